@@ -1,0 +1,229 @@
+"""Benchmark: the L 64x8 MoE FFN layer forward at 16384 tokens on one MI355X.
+
+A step is one forward pass of the whole MoE FFN layer (models/layers.py:596-634):
+gate GEMM, router kernel, dispatch, fused gather + gate_up GEMM + SwiGLU,
+down GEMM and combine, over 16384 bf16 tokens of N(0,1) with N(0, 0.02)
+weights (H=1280, E=64, I=448, top-8).  Inputs stay resident in HBM.
+Consecutive steps alternate between weight copies so the 256 MB
+Infinity Cache cannot keep one layer's 220 MB of expert weights.
+
+Printed (one JSON line on stdout): active TFLOP/s of the layer (6*R*H*I per
+step, R = T*k), ms per layer, the roofline of the dominant kernel (fused
+gate_up + SwiGLU GEMM, timed with events on its stream) and the reference's
+eager CPU path timed on the host's cores over a bounded sample.
+
+Usage: python bench.py [--steps K] [--warmup W] [--gpus 1] [--workload l64x8|xl_skew|xl128|decode_T]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+
+import torch
+import torch.nn.functional as F
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+METRIC = "MoE FFN ms/layer + active TFLOP/s (% bf16 MFMA peak), L 64x8, 16k tokens"
+PEAK_BF16_TFLOPS = 2500.0  # MI355X dense bf16 MFMA (published)
+PEAK_HBM_GBS = 8000.0
+
+WORKLOADS = {
+    # name: (tokens, hidden, experts, inter, top_k, logit bias std)
+    "l64x8": (16384, 1280, 64, 448, 8, 0.0),
+    "xl_skew": (16384, 1536, 64, 512, 8, 1.5),
+    "xl128": (32768, 1536, 128, 512, 8, 0.0),
+}
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def make_layer(hrm, dev, t, h, e, i, k, bias_std, seed):
+    g = torch.Generator(device=dev).manual_seed(seed)
+    layer = hrm.SparseMoESwiGLU(h, i, e, k, True, implementation="grouped_triton").to(dev, torch.bfloat16)
+    with torch.no_grad():
+        layer.gate.weight.normal_(0.0, 0.02, generator=g)
+        layer.experts.gate_up_weight.normal_(0.0, 0.02, generator=g)
+        layer.experts.down_weight.normal_(0.0, 0.02, generator=g)
+        x = torch.randn(t, h, device=dev, generator=g).to(torch.bfloat16)
+        if bias_std > 0:
+            b = torch.randn(e, device=dev, generator=g) * bias_std
+            wg = layer.gate.weight.double()
+            v = wg.T @ torch.linalg.solve(wg @ wg.T, b.double())
+            x = (x.double() + v[None, :]).to(torch.bfloat16)
+    return layer, x
+
+
+def time_layers(layers, xs, steps, warmup):
+    with torch.no_grad():
+        for s in range(warmup):
+            layers[s % len(layers)](xs[s % len(xs)])
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        start = torch.cuda.Event(enable_timing=True)
+        end = torch.cuda.Event(enable_timing=True)
+        start.record()
+        for s in range(steps):
+            layers[s % len(layers)](xs[s % len(xs)])
+        end.record()
+        torch.cuda.synchronize()
+        wall = time.perf_counter() - t0
+    return start.elapsed_time(end) / steps, wall
+
+
+def phase_times(hrm, layer, x, reps=10):
+    """Per-kernel averages with events on torch's current stream (the stream every op launches on)."""
+    from hrm_moe_amd import ops
+
+    k, e = layer.top_k, layer.num_experts
+    w_gu, w_dn = layer.experts.gate_up_weight, layer.experts.down_weight
+    names = ["gate_gemm", "router", "dispatch", "gate_up_swiglu", "down_gemm", "combine"]
+    acc = {n: [] for n in names}
+    with torch.no_grad():
+        for _ in range(reps + 2):
+            ev = [torch.cuda.Event(enable_timing=True) for _ in range(len(names) + 1)]
+            ev[0].record()
+            logits = F.linear(x, layer.gate.weight)
+            ev[1].record()
+            _, w, idx = ops.router_topk(logits, k, True, x.dtype, want_probs=False)
+            ev[2].record()
+            d = ops.permute(idx, e)
+            ev[3].record()
+            act = ops.gate_up_swiglu(x, d, w_gu)
+            ev[4].record()
+            y = ops.grouped_gemm_nt(act, w_dn, d.tokens_per_expert)
+            ev[5].record()
+            ops.combine(y, d, w)
+            ev[6].record()
+            torch.cuda.synchronize()
+            for j, n in enumerate(names):
+                acc[n].append(ev[j].elapsed_time(ev[j + 1]))
+    return {n: statistics.median(v[2:]) for n, v in acc.items()}
+
+
+def read_traffic(name):
+    """HBM bytes per launch from a committed rocprofv3 --pmc summary, if one exists."""
+    path = os.path.join(ROOT, "profiles", name)
+    if not os.path.exists(path):
+        return None
+    for line in open(path):
+        if line.startswith("hbm_bytes_per_launch:"):
+            return int(float(line.split(":", 1)[1].strip()))
+    return None
+
+
+def cpu_baseline(t, h, e, i, k, sample_tokens=2048, runs=5):
+    """The reference's eager CPU path (oracle.moe_forward_eager) on a bounded sample of the workload."""
+    from oracle import moe_oracle, synth
+
+    x, wg, wgu, wdn = synth.moe_inputs(1, sample_tokens, h, e, i)
+    args = [torch.from_numpy(a).to(torch.bfloat16) for a in (x, wg, wgu, wdn)]
+    moe_oracle.moe_forward_eager(*args, k)
+    ts = []
+    for _ in range(runs):
+        t0 = time.perf_counter()
+        moe_oracle.moe_forward_eager(*args, k)
+        ts.append(time.perf_counter() - t0)
+    sec = statistics.median(ts)
+    flops = 6.0 * sample_tokens * k * h * i
+    try:
+        affinity = len(os.sched_getaffinity(0))
+    except AttributeError:
+        affinity = os.cpu_count()
+    return {
+        "value": round(flops / sec / 1e12, 5),
+        "unit": "TFLOP/s",
+        "cores": torch.get_num_threads(),
+        "kind": "port",
+        "sample": (f"{sample_tokens} of {t} tokens of the same layer shape, bf16, reference eager CPU path "
+                   f"(per-expert F.linear), median of {runs} runs after 1 warmup: {sec * 1e3:.1f} ms; "
+                   f"os.cpu_count()={os.cpu_count()}, affinity={affinity}"),
+        "ms_per_layer_extrapolated": round(sec * 1e3 * t / sample_tokens, 1),
+    }
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--workload", default="l64x8", choices=sorted(WORKLOADS))
+    ap.add_argument("--weight-copies", type=int, default=2)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU: this build has no multi-GPU path (run with --gpus 1)", file=sys.stderr)
+        sys.exit(2)
+    assert torch.cuda.is_available(), "bench.py needs a ROCm GPU"
+
+    import hrm_moe_amd as hrm
+
+    hrm.load_library()
+    dev = torch.device("cuda:0")
+    t, h, e, i, k, bias = WORKLOADS[args.workload]
+    r = t * k
+    layers, xs = [], []
+    for c in range(max(1, args.weight_copies)):
+        layer, x = make_layer(hrm, dev, t, h, e, i, k, bias, seed=1234 + c)
+        layers.append(layer)
+        xs.append(x)
+    ms, wall = time_layers(layers, xs, args.steps, args.warmup)
+    flops = 6.0 * r * h * i
+    tflops = flops / (ms * 1e-3) / 1e12
+
+    phases = phase_times(hrm, layers[0], xs[0])
+    gate_up_ms = phases["gate_up_swiglu"]
+    gate_up_flops = 4.0 * r * h * i
+    achieved = gate_up_flops / (gate_up_ms * 1e-3) / 1e12
+    log("phase medians (ms): " + ", ".join(f"{n} {v:.4f}" for n, v in phases.items()))
+    log(f"layer {ms:.4f} ms ({wall / args.steps * 1e3:.4f} ms wall per step), {tflops:.1f} TFLOP/s active, "
+        f"{100 * tflops / PEAK_BF16_TFLOPS:.1f}% of bf16 peak")
+
+    result = {
+        "metric": METRIC,
+        "value": round(tflops, 2),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {
+            "workload": f"{args.workload}: MoE FFN layer forward, {t} tokens, H={h}, E={e}, I={i}, top-{k}, "
+                        f"fp32 router" + (f", logit bias N(0,{bias})" if bias else ""),
+            "tokens": t, "hidden": h, "experts": e, "inter": i, "top_k": k,
+            "weight_copies": len(layers),
+        },
+        "ms_per_layer": round(ms, 5),
+        "pct_bf16_peak": round(100 * tflops / PEAK_BF16_TFLOPS, 2),
+        "phase_ms": {n: round(v, 5) for n, v in phases.items()},
+        "roofline": {
+            "kernel": "mgemm_kernel<BF16, GATHER_SWIGLU, 256, 128> (fused gather + gate_up GEMM + SwiGLU) + its plan kernel",
+            "bound": "mfma",
+            "achieved": round(achieved, 2),
+            "peak": PEAK_BF16_TFLOPS,
+            "unit": "TFLOP/s",
+            "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
+            "traffic": read_traffic(f"gate_up_swiglu_{args.workload}_traffic.txt"),
+            "flops_per_launch": gate_up_flops,
+            "avg_launch_ms": round(gate_up_ms, 5),
+        },
+    }
+    if not args.no_cpu_baseline:
+        result["cpu_baseline"] = cpu_baseline(t, h, e, i, k)
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,136 @@
+// Weighted combine of expert rows back to token order.
+//
+// Replaces models/layers.py:333-334 of the reference:
+//   expert_output = expert_output * sorted_weights[:, None]
+//   final_hidden_states.index_add_(0, sorted_token_idx, expert_output)
+// as a gather instead of a scatter: one wavefront per token reads the token's
+// k rows (slot_to_row), multiplies each by its routing weight with a rounding
+// to the element type (the reference multiplies 16-bit tensors), and adds the
+// products in fp32 in ascending row order, rounding once at the end.  That is
+// the arithmetic of the reference's index_add_ on the CPU.  The gather does
+// no atomics, so the result is the same on every run.
+#include "common.h"
+
+namespace hrm {
+namespace {
+
+template <int DT>
+struct Elem;
+template <>
+struct Elem<HRM_MOE_BF16> {
+  static constexpr int kPer16 = 8;
+  static __device__ __forceinline__ float get(const u32x4& v, int q) {
+    const uint32_t w = v[q >> 1];
+    return BF16::to_f((uint16_t)((q & 1) ? (w >> 16) : (w & 0xffff)));
+  }
+  static __device__ __forceinline__ float round(float f) { return BF16::to_f(BF16::from_f(f)); }
+  static __device__ __forceinline__ float weight(const void* p, int64_t i) { return BF16::to_f(reinterpret_cast<const uint16_t*>(p)[i]); }
+  static __device__ __forceinline__ u32x4 pack(const float* a) {
+    return u32x4{pack2(BF16::from_f(a[0]), BF16::from_f(a[1])), pack2(BF16::from_f(a[2]), BF16::from_f(a[3])),
+                 pack2(BF16::from_f(a[4]), BF16::from_f(a[5])), pack2(BF16::from_f(a[6]), BF16::from_f(a[7]))};
+  }
+};
+template <>
+struct Elem<HRM_MOE_F16> {
+  static constexpr int kPer16 = 8;
+  static __device__ __forceinline__ float get(const u32x4& v, int q) {
+    const uint32_t w = v[q >> 1];
+    return F16::to_f((uint16_t)((q & 1) ? (w >> 16) : (w & 0xffff)));
+  }
+  static __device__ __forceinline__ float round(float f) { return F16::to_f(F16::from_f(f)); }
+  static __device__ __forceinline__ float weight(const void* p, int64_t i) { return F16::to_f(reinterpret_cast<const uint16_t*>(p)[i]); }
+  static __device__ __forceinline__ u32x4 pack(const float* a) {
+    return u32x4{pack2(F16::from_f(a[0]), F16::from_f(a[1])), pack2(F16::from_f(a[2]), F16::from_f(a[3])),
+                 pack2(F16::from_f(a[4]), F16::from_f(a[5])), pack2(F16::from_f(a[6]), F16::from_f(a[7]))};
+  }
+};
+template <>
+struct Elem<HRM_MOE_F32> {
+  static constexpr int kPer16 = 4;
+  static __device__ __forceinline__ float get(const u32x4& v, int q) { return __uint_as_float(v[q]); }
+  static __device__ __forceinline__ float round(float f) { return f; }
+  static __device__ __forceinline__ float weight(const void* p, int64_t i) { return reinterpret_cast<const float*>(p)[i]; }
+  static __device__ __forceinline__ u32x4 pack(const float* a) {
+    return u32x4{__float_as_uint(a[0]), __float_as_uint(a[1]), __float_as_uint(a[2]), __float_as_uint(a[3])};
+  }
+};
+
+constexpr int kWavesPerBlock = 4;
+constexpr int kMaxTopK = 32;
+
+template <int DT>
+__global__ __launch_bounds__(kWavesPerBlock * 64) void combine_kernel(const char* __restrict__ Y,
+                                                                     const int32_t* __restrict__ slot_to_row,
+                                                                     const void* __restrict__ wts,
+                                                                     const int32_t* __restrict__ expert_offsets,
+                                                                     int64_t T, int k, int64_t H, int E,
+                                                                     char* __restrict__ out) {
+  using El = Elem<DT>;
+  constexpr int P = El::kPer16;
+  constexpr int ESZ = 16 / P;
+  __shared__ int32_t s_row[kWavesPerBlock][kMaxTopK];
+  __shared__ float s_w[kWavesPerBlock][kMaxTopK];
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  const int64_t t = (int64_t)blockIdx.x * kWavesPerBlock + wv;
+  const bool active = t < T;  // every wave reaches the barrier
+  const int32_t r_valid = expert_offsets[E];
+  int32_t row = 0x7fffffff;
+  float w = 0.0f;
+  if (active && lane < k) {
+    row = slot_to_row[t * k + lane];
+    w = El::weight(wts, t * k + lane);
+  }
+  // Rank of this lane's row among the token's k rows (rows are distinct).
+  int rank = 0;
+  for (int j = 0; j < k; ++j) {
+    const int32_t other = __shfl(row, j);
+    rank += (other < row) ? 1 : 0;
+  }
+  if (active && lane < k) {
+    s_row[wv][rank] = row;
+    s_w[wv][rank] = w;
+  }
+  __syncthreads();
+  if (!active) return;
+  const int64_t chunks = H / P;
+  for (int64_t c = lane; c < chunks; c += 64) {
+    float acc[P];
+#pragma unroll
+    for (int q = 0; q < P; ++q) acc[q] = 0.0f;
+    for (int j = 0; j < k; ++j) {
+      const int32_t r = s_row[wv][j];
+      if (r >= r_valid) continue;
+      const float wj = s_w[wv][j];
+      const u32x4 y = ld16(Y + ((int64_t)r * H + c * P) * ESZ);
+#pragma unroll
+      for (int q = 0; q < P; ++q) acc[q] += El::round(El::get(y, q) * wj);
+    }
+    st16(out + (t * H + c * P) * ESZ, El::pack(acc));
+  }
+}
+
+}  // namespace
+}  // namespace hrm
+
+extern "C" int hrm_moe_combine(const void* expert_out, const int32_t* slot_to_row, const void* topk_weight,
+                               const int32_t* expert_offsets, int64_t num_tokens, int32_t top_k, int64_t hidden_size,
+                               int32_t num_experts, int dtype, void* out, void* stream) {
+  if (num_tokens < 0 || top_k < 1 || hidden_size < 1 || num_experts < 1) return HRM_MOE_ERR_INVALID;
+  if (dtype < HRM_MOE_BF16 || dtype > HRM_MOE_F32) return HRM_MOE_ERR_DTYPE;
+  if (top_k > hrm::kMaxTopK || hidden_size % 8) return HRM_MOE_ERR_UNSUPPORTED;
+  if (num_tokens == 0) return HRM_MOE_OK;
+  if (!expert_out || !slot_to_row || !topk_weight || !expert_offsets || !out) return HRM_MOE_ERR_INVALID;
+  dim3 grid((unsigned)((num_tokens + hrm::kWavesPerBlock - 1) / hrm::kWavesPerBlock)), block(hrm::kWavesPerBlock * 64);
+  const char* Y = static_cast<const char*>(expert_out);
+  char* O = static_cast<char*>(out);
+  if (dtype == HRM_MOE_BF16)
+    HRM_LAUNCH(hrm::combine_kernel<HRM_MOE_BF16>, grid, block, 0, stream, Y, slot_to_row, topk_weight, expert_offsets,
+               num_tokens, top_k, hidden_size, num_experts, O);
+  else if (dtype == HRM_MOE_F16)
+    HRM_LAUNCH(hrm::combine_kernel<HRM_MOE_F16>, grid, block, 0, stream, Y, slot_to_row, topk_weight, expert_offsets,
+               num_tokens, top_k, hidden_size, num_experts, O);
+  else
+    HRM_LAUNCH(hrm::combine_kernel<HRM_MOE_F32>, grid, block, 0, stream, Y, slot_to_row, topk_weight, expert_offsets,
+               num_tokens, top_k, hidden_size, num_experts, O);
+  return HRM_MOE_OK;
+}

@@ -1,0 +1,60 @@
+// Shared device types and helpers for the gfx950 MoE kernels.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "hrm_moe.h"
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 halfx8 __attribute__((ext_vector_type(8)));
+typedef short shortx4 __attribute__((ext_vector_type(4)));
+typedef float floatx16 __attribute__((ext_vector_type(16)));
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+#define HRM_LDS __attribute__((address_space(3)))
+
+namespace hrm {
+
+constexpr int kWave = 64;
+
+// 16-bit element types the GEMMs accept.  Storage is raw 16-bit; the traits
+// give the MFMA and the conversions.
+struct BF16 {
+  static __device__ __forceinline__ float to_f(uint16_t v) { return __uint_as_float(uint32_t(v) << 16); }
+  static __device__ __forceinline__ uint16_t from_f(float f) {
+    __bf16 b = static_cast<__bf16>(f);  // round to nearest even (v_cvt_pk_bf16_f32)
+    return __builtin_bit_cast(uint16_t, b);
+  }
+  static __device__ __forceinline__ floatx16 mfma32(u32x4 a, u32x4 b, floatx16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+  }
+};
+
+struct F16 {
+  static __device__ __forceinline__ float to_f(uint16_t v) { return float(__builtin_bit_cast(_Float16, v)); }
+  static __device__ __forceinline__ uint16_t from_f(float f) { return __builtin_bit_cast(uint16_t, static_cast<_Float16>(f)); }
+  static __device__ __forceinline__ floatx16 mfma32(u32x4 a, u32x4 b, floatx16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(halfx8, a), __builtin_bit_cast(halfx8, b), c, 0, 0, 0);
+  }
+};
+
+__device__ __forceinline__ uint32_t pack2(uint16_t lo, uint16_t hi) { return uint32_t(lo) | (uint32_t(hi) << 16); }
+
+// 16-byte global load / store helpers (addresses must be 16-byte aligned).
+__device__ __forceinline__ u32x4 ld16(const void* p) { return *reinterpret_cast<const u32x4*>(p); }
+__device__ __forceinline__ void st16(void* p, u32x4 v) { *reinterpret_cast<u32x4*>(p) = v; }
+__device__ __forceinline__ void st8(void* p, u32x2 v) { *reinterpret_cast<u32x2*>(p) = v; }
+
+inline int ceil_div(int64_t a, int64_t b) { return int((a + b - 1) / b); }
+
+}  // namespace hrm
+
+// Launch helper: returns the launch status as an int.
+#define HRM_LAUNCH(kernel, grid, block, shmem, stream, ...)                                   \
+  do {                                                                                          \
+    hipLaunchKernelGGL(kernel, grid, block, shmem, (hipStream_t)(stream), __VA_ARGS__);         \
+    hipError_t e_ = hipGetLastError();                                                          \
+    if (e_ != hipSuccess) return int(e_);                                                       \
+  } while (0)

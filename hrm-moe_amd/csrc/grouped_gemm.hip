@@ -1,0 +1,636 @@
+// Grouped GEMMs over expert-contiguous rows, for gfx950 MFMA.
+//
+// Replaces the reference's Triton kernels (models/moe_triton_grouped_gemm.py):
+//   _m_grouped_gemm_bk_kernel :113-184  -> KIND_NT       (C = A . W[e]^T)
+//   _m_grouped_gemm_bn_kernel :187-260  -> KIND_NN       (C = A . W[e], dgrad)
+//   _k_grouped_gemm_kernel    :277-347  -> wgrad kernel  (C[e] = A_e^T . B_e)
+//   _repeat_interleave_kernel :263-274  -> plan kernel   (tile table on device)
+// plus KIND_GATHER_SWIGLU, which fuses the row gather and the SwiGLU of
+// models/layers.py:320,326-329 into the gate_up GEMM.
+//
+// Work decomposition
+//  * A plan kernel turns tokens_per_expert (device int64) into a table of
+//    M-tiles {expert, first row, end row}, so nothing is read on the host.
+//  * M-grouped kernels are persistent.  Workgroup w runs on XCD w % 8, and
+//    each XCD owns one contiguous eighth of the tile list (M-tile major,
+//    N-tile minor), so an expert's weights stay in one XCD's L2.
+//  * A workgroup is 4 waves (2 x 2).  It computes a BM x BN tile; each wave owns
+//    (BM/2) x (BN/2) as 32x32 MFMA blocks of v_mfma_f32_32x32x16_{bf16,f16}.
+//    Operand roles are swapped (W rows feed the MFMA A operand) so each lane
+//    ends with four consecutive output columns and stores 8 bytes.
+//  * K is consumed 64 at a time through two LDS stages.  Row-major K-contiguous
+//    tiles are stored as [rows][64] with the 16-byte chunk index XORed by
+//    (row & 7).  K-strided tiles (dgrad's W, both wgrad operands) are stored
+//    as [k][cols] and read with ds_read_b64_tr_b16, which transposes 4x16
+//    blocks of 16-bit values inside each 16-lane group.
+#include "common.h"
+
+namespace hrm {
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kBK = 64;
+constexpr int kMaxExperts = 1024;
+
+enum { KIND_NT = 0, KIND_GATHER_SWIGLU = 1, KIND_NN = 2 };
+
+struct MTile {
+  int32_t expert, row_start, row_end, pad;
+};
+
+inline size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
+
+// ---------------------------------------------------------------------------
+// Plan: tile table from tokens_per_expert
+// ---------------------------------------------------------------------------
+// Writes tiles[0..count) and count, plus row_offsets[0..E] (exclusive prefix of
+// clamped counts).  Rows are clamped to [0, M): a tokens_per_expert that sums
+// past M never makes a kernel touch rows >= M.  Also zeroes the work counter.
+__global__ __launch_bounds__(1024) void plan_kernel(const int64_t* __restrict__ tpe, int E, int64_t M, int BM,
+                                                    MTile* __restrict__ tiles, int max_tiles, int* __restrict__ count,
+                                                    int* __restrict__ row_offsets, int* __restrict__ work_counter) {
+  __shared__ int64_t s_rows[kMaxExperts + 1];
+  __shared__ int s_ntile[kMaxExperts + 1];
+  __shared__ int s_rs[kMaxExperts];
+  __shared__ int s_re[kMaxExperts];
+  const int tid = threadIdx.x;
+  for (int e = tid; e < E; e += blockDim.x) {
+    int64_t n = tpe[e];
+    s_rows[e] = n > 0 ? n : 0;
+  }
+  __syncthreads();
+  // Inclusive Hillis-Steele scan of row counts over E <= 1024 entries.
+  for (int off = 1; off < E; off *= 2) {
+    int64_t v = 0;
+    if (tid < E && tid >= off) v = s_rows[tid - off];
+    __syncthreads();
+    if (tid < E && tid >= off) s_rows[tid] += v;
+    __syncthreads();
+  }
+  if (tid < E) {
+    const int64_t end = s_rows[tid];
+    const int64_t n = tid == 0 ? end : end - s_rows[tid - 1];
+    int64_t rs = end - n, re = end;
+    rs = rs < M ? rs : M;
+    re = re < M ? re : M;
+    s_rs[tid] = (int)rs;
+    s_re[tid] = (int)re;
+    s_ntile[tid] = (int)((re - rs + BM - 1) / BM);
+    row_offsets[tid] = (int)rs;
+    if (tid == E - 1) row_offsets[E] = (int)re;
+  }
+  __syncthreads();
+  for (int off = 1; off < E; off *= 2) {
+    int v = 0;
+    if (tid < E && tid >= off) v = s_ntile[tid - off];
+    __syncthreads();
+    if (tid < E && tid >= off) s_ntile[tid] += v;
+    __syncthreads();
+  }
+  int total = s_ntile[E - 1];
+  total = total < max_tiles ? total : max_tiles;
+  for (int i = tid; i < total; i += blockDim.x) {
+    int lo = 0, hi = E - 1;  // first e with inclusive prefix > i
+    while (lo < hi) {
+      const int mid = (lo + hi) >> 1;
+      if (s_ntile[mid] > i) hi = mid; else lo = mid + 1;
+    }
+    const int before = lo == 0 ? 0 : s_ntile[lo - 1];
+    const int j = i - before;
+    MTile t;
+    t.expert = lo;
+    t.row_start = s_rs[lo] + j * BM;
+    const int e2 = t.row_start + BM;
+    t.row_end = e2 < s_re[lo] ? e2 : s_re[lo];
+    t.pad = 0;
+    tiles[i] = t;
+  }
+  if (tid == 0) {
+    *count = total;
+    *work_counter = 0;
+  }
+}
+
+struct GemmWs {
+  MTile* tiles;
+  int* count;
+  int* row_offsets;
+  int* work_counter;
+};
+
+inline size_t gemm_ws_bytes(int64_t M, int E, int bm_min) {
+  const int64_t max_tiles = (M + bm_min - 1) / bm_min + E;
+  return align256(sizeof(MTile) * (size_t)max_tiles) + align256(sizeof(int) * 4) + align256(sizeof(int) * (E + 1));
+}
+
+inline GemmWs carve(void* ws, int64_t M, int E, int bm_min) {
+  const int64_t max_tiles = (M + bm_min - 1) / bm_min + E;
+  char* p = static_cast<char*>(ws);
+  GemmWs w;
+  w.tiles = reinterpret_cast<MTile*>(p);
+  p += align256(sizeof(MTile) * (size_t)max_tiles);
+  w.count = reinterpret_cast<int*>(p);
+  w.work_counter = w.count + 1;
+  p += align256(sizeof(int) * 4);
+  w.row_offsets = reinterpret_cast<int*>(p);
+  return w;
+}
+
+// ---------------------------------------------------------------------------
+// LDS addressing
+// ---------------------------------------------------------------------------
+// [rows][64] tile, K contiguous: 128 B per row, 16-byte chunk c at (c ^ (row & 7)).
+__device__ __forceinline__ uint32_t kc_off(int row, int chunk) { return uint32_t(row * 128 + ((chunk ^ (row & 7)) << 4)); }
+// [64 k][COLS] tile, columns contiguous: 16-byte chunk c of row k at (c ^ ((k & 3) << 1)).
+template <int COLS>
+__device__ __forceinline__ uint32_t kr_off(int k, int chunk) { return uint32_t(k * (COLS * 2) + ((chunk ^ ((k & 3) << 1)) << 4)); }
+
+// LDS pointers are plain pointers into __shared__ arrays; the compiler infers
+// the LDS address space.  The transpose load takes an explicit LDS pointer.
+__device__ __forceinline__ u32x4 lds_read16(const char* base, uint32_t off) {
+  return *reinterpret_cast<const u32x4*>(base + off);
+}
+__device__ __forceinline__ void lds_write16(char* base, uint32_t off, u32x4 v) {
+  *reinterpret_cast<u32x4*>(base + off) = v;
+}
+__device__ __forceinline__ u32x2 lds_read_tr16(const char* base, uint32_t off) {
+  shortx4 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((HRM_LDS shortx4*)(base + off));
+  return __builtin_bit_cast(u32x2, v);
+}
+
+// MFMA operand (8 values along the reduction) for output index i = l % 32 of a
+// 32-wide block whose columns start at col0, from a [64 k][COLS] tile, at
+// reduction sub-step s (16 values).  Lane l of 16-lane group g reads row
+// k = s*16 + (g>>1)*8 + kk + (i>>2), columns col0 + (g&1)*16 + 4*(i&3) .. +3;
+// the transpose hands lane j of the group column col0 + (g&1)*16 + j.
+template <int COLS>
+__device__ __forceinline__ u32x4 tr_operand(const char* base, int col0, int s, int lane) {
+  const int g = lane >> 4, i = lane & 15;
+  const int col = col0 + (g & 1) * 16 + 4 * (i & 3);
+  const int kb = s * 16 + (g >> 1) * 8 + (i >> 2);
+  const uint32_t o0 = kr_off<COLS>(kb, col >> 3) + (col & 7) * 2;
+  const uint32_t o1 = kr_off<COLS>(kb + 4, col >> 3) + (col & 7) * 2;
+  const u32x2 lo = lds_read_tr16(base, o0);
+  const u32x2 hi = lds_read_tr16(base, o1);
+  return u32x4{lo.x, lo.y, hi.x, hi.y};
+}
+
+template <typename TR>
+__device__ __forceinline__ u32x2 pack4(float a, float b, float c, float d) {
+  return u32x2{pack2(TR::from_f(a), TR::from_f(b)), pack2(TR::from_f(c), TR::from_f(d))};
+}
+
+// silu(gate) * up with the reference's roundings: gate, up, silu(gate) and the
+// product are each rounded to the element type (models/layers.py:328-329 on
+// 16-bit tensors; torch's silu computes x / (1 + exp(-x)) in fp32).
+template <typename TR>
+__device__ __forceinline__ float swiglu_ref(float g, float u) {
+  const float gr = TR::to_f(TR::from_f(g));
+  const float ur = TR::to_f(TR::from_f(u));
+  const float s = TR::to_f(TR::from_f(gr / (1.0f + expf(-gr))));
+  return s * ur;
+}
+
+// ---------------------------------------------------------------------------
+// M-grouped GEMM (persistent)
+// ---------------------------------------------------------------------------
+// KIND_NT:            C[M,N]  = A[M,K] . W[e][N,K]^T
+// KIND_GATHER_SWIGLU: C[M,I]  = swiglu(A[gather[m]] . W[e][2I,K]^T), N = I
+// KIND_NN:            C[M,N]  = A[M,K] . W[e][K,N]
+template <typename TR, int KIND, int BM, int BN>
+__global__ __launch_bounds__(kThreads, 1) void mgemm_kernel(const uint16_t* __restrict__ A,
+                                                           const int32_t* __restrict__ gather,
+                                                           const uint16_t* __restrict__ W, uint16_t* __restrict__ C,
+                                                           const MTile* __restrict__ tiles,
+                                                           const int* __restrict__ tile_count, int N, int K,
+                                                           int tiles_n) {
+  constexpr int MB = BM / 64;  // 32-row blocks per wave
+  constexpr int NB = BN / 64;  // 32-col blocks per wave
+  constexpr int A_BYTES = BM * kBK * 2;
+  constexpr int B_BYTES = BN * kBK * 2;
+  constexpr int A_LOADS = BM / 32;                       // 16-byte loads per thread per stage
+  constexpr int B_LOADS = KIND == KIND_NN ? 4 : BN / 32;  // NN: 64 k-rows x BN/8 chunks
+  static_assert(KIND != KIND_NN || BN == 128, "NN tile loader assumes BN == 128");
+  __shared__ __attribute__((aligned(16))) char smem[2 * (A_BYTES + B_BYTES)];
+  char* lds = smem;
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int wm = wave >> 1, wn = wave & 1;
+
+  const int total = (*tile_count) * tiles_n;
+  const int xcd = blockIdx.x & 7;
+  const int nloc = gridDim.x >> 3;
+  const int chunk = (total + 7) >> 3;
+  const int64_t w_rows = KIND == KIND_GATHER_SWIGLU ? 2 * (int64_t)N : (KIND == KIND_NN ? (int64_t)K : (int64_t)N);
+  const int64_t w_cols = KIND == KIND_NN ? (int64_t)N : (int64_t)K;
+  const int nk = (K + kBK - 1) / kBK;
+
+  for (int j = blockIdx.x >> 3; j < chunk; j += nloc) {
+    const int t = xcd * chunk + j;
+    if (t >= total) break;
+    const MTile ti = tiles[t / tiles_n];
+    const int nt = t - (t / tiles_n) * tiles_n;
+    const int rs = ti.row_start, re = ti.row_end;
+    const uint16_t* Wexp = W + (int64_t)ti.expert * w_rows * w_cols;
+
+    // ---- global source pointers for this tile
+    const uint16_t* a_src[A_LOADS];
+    const int ca = tid & 7;
+#pragma unroll
+    for (int i = 0; i < A_LOADS; ++i) {
+      int r = rs + (tid >> 3) + 32 * i;
+      r = r < re ? r : re - 1;
+      const int64_t src = KIND == KIND_GATHER_SWIGLU ? (int64_t)gather[r] : (int64_t)r;
+      a_src[i] = A + src * K + ca * 8;
+    }
+    const uint16_t* b_src[B_LOADS];
+    int n0;
+    if constexpr (KIND == KIND_NN) {
+      n0 = nt * BN;
+      int col = n0 + (tid & 15) * 8;
+      col = col < N ? col : N - 8;
+#pragma unroll
+      for (int i = 0; i < B_LOADS; ++i) b_src[i] = Wexp + (int64_t)((tid >> 4) + 16 * i) * N + col;
+    } else if constexpr (KIND == KIND_GATHER_SWIGLU) {
+      n0 = nt * (BN / 2);  // first intermediate column of the tile
+#pragma unroll
+      for (int i = 0; i < B_LOADS; ++i) {
+        const int jr = (tid >> 3) + 32 * i;  // 0..BN-1: first half gate rows, second half up rows
+        int c = n0 + (jr % (BN / 2));
+        c = c < N ? c : N - 1;
+        const int64_t wr = jr < BN / 2 ? c : (int64_t)N + c;
+        b_src[i] = Wexp + wr * K + ca * 8;
+      }
+    } else {
+      n0 = nt * BN;
+#pragma unroll
+      for (int i = 0; i < B_LOADS; ++i) {
+        int n = n0 + (tid >> 3) + 32 * i;
+        n = n < N ? n : N - 1;
+        b_src[i] = Wexp + (int64_t)n * K + ca * 8;
+      }
+    }
+
+    u32x4 ra[A_LOADS], rb[B_LOADS];
+    auto gload = [&](int kt) {
+      const int k0 = kt * kBK;
+      const bool ka_ok = k0 + ca * 8 < K;
+#pragma unroll
+      for (int i = 0; i < A_LOADS; ++i) ra[i] = ka_ok ? ld16(a_src[i] + k0) : u32x4{0, 0, 0, 0};
+      if constexpr (KIND == KIND_NN) {
+#pragma unroll
+        for (int i = 0; i < B_LOADS; ++i) {
+          const int kr = k0 + (tid >> 4) + 16 * i;
+          rb[i] = kr < K ? ld16(b_src[i] + (int64_t)k0 * N) : u32x4{0, 0, 0, 0};
+        }
+      } else {
+#pragma unroll
+        for (int i = 0; i < B_LOADS; ++i) rb[i] = ka_ok ? ld16(b_src[i] + k0) : u32x4{0, 0, 0, 0};
+      }
+    };
+    auto sstore = [&](int buf) {
+      char* la = lds + buf * (A_BYTES + B_BYTES);
+      char* lb = la + A_BYTES;
+#pragma unroll
+      for (int i = 0; i < A_LOADS; ++i) lds_write16(la, kc_off((tid >> 3) + 32 * i, ca), ra[i]);
+      if constexpr (KIND == KIND_NN) {
+#pragma unroll
+        for (int i = 0; i < B_LOADS; ++i) lds_write16(lb, kr_off<BN>((tid >> 4) + 16 * i, tid & 15), rb[i]);
+      } else {
+#pragma unroll
+        for (int i = 0; i < B_LOADS; ++i) lds_write16(lb, kc_off((tid >> 3) + 32 * i, ca), rb[i]);
+      }
+    };
+
+    floatx16 acc[NB][MB];
+#pragma unroll
+    for (int b = 0; b < NB; ++b)
+#pragma unroll
+      for (int a = 0; a < MB; ++a)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) acc[b][a][v] = 0.0f;
+
+    gload(0);
+    sstore(0);
+    __syncthreads();
+    for (int kt = 0; kt < nk; ++kt) {
+      if (kt + 1 < nk) gload(kt + 1);
+      const char* la = lds + (kt & 1) * (A_BYTES + B_BYTES);
+      const char* lb = la + A_BYTES;
+#pragma unroll
+      for (int s = 0; s < kBK / 16; ++s) {
+        u32x4 fw[NB], fa[MB];
+#pragma unroll
+        for (int b = 0; b < NB; ++b) {
+          int r0;
+          if constexpr (KIND == KIND_GATHER_SWIGLU) r0 = b * (BN / 2) + wn * 32;
+          else r0 = wn * (BN / 2) + b * 32;
+          if constexpr (KIND == KIND_NN) fw[b] = tr_operand<BN>(lb, r0, s, lane);
+          else fw[b] = lds_read16(lb, kc_off(r0 + (lane & 31), s * 2 + (lane >> 5)));
+        }
+#pragma unroll
+        for (int a = 0; a < MB; ++a) {
+          const int r = wm * (BM / 2) + a * 32 + (lane & 31);
+          fa[a] = lds_read16(la, kc_off(r, s * 2 + (lane >> 5)));
+        }
+#pragma unroll
+        for (int b = 0; b < NB; ++b)
+#pragma unroll
+          for (int a = 0; a < MB; ++a) acc[b][a] = TR::mfma32(fw[b], fa[a], acc[b][a]);
+      }
+      if (kt + 1 < nk) sstore((kt + 1) & 1);
+      __syncthreads();
+    }
+
+    // ---- epilogue: lane holds rows m = base + (lane & 31), columns g*8 + (lane>>5)*4 + 0..3
+#pragma unroll
+    for (int a = 0; a < MB; ++a) {
+      const int m = rs + wm * (BM / 2) + a * 32 + (lane & 31);
+      if (m >= re) continue;
+      if constexpr (KIND == KIND_GATHER_SWIGLU) {
+        uint16_t* crow = C + (int64_t)m * N;
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const int c = n0 + wn * 32 + g * 8 + (lane >> 5) * 4;
+          if (c < N) {
+            float o[4];
+#pragma unroll
+            for (int q = 0; q < 4; ++q) o[q] = swiglu_ref<TR>(acc[0][a][g * 4 + q], acc[1][a][g * 4 + q]);
+            st8(crow + c, pack4<TR>(o[0], o[1], o[2], o[3]));
+          }
+        }
+      } else {
+        uint16_t* crow = C + (int64_t)m * N;
+#pragma unroll
+        for (int b = 0; b < NB; ++b)
+#pragma unroll
+          for (int g = 0; g < 4; ++g) {
+            const int c = n0 + wn * (BN / 2) + b * 32 + g * 8 + (lane >> 5) * 4;
+            if (c < N)
+              st8(crow + c, pack4<TR>(acc[b][a][g * 4 + 0], acc[b][a][g * 4 + 1], acc[b][a][g * 4 + 2],
+                                      acc[b][a][g * 4 + 3]));
+          }
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Wgrad: C[e][Na,Nb] = A[rows_e]^T . B[rows_e]  (persistent, work queue)
+// ---------------------------------------------------------------------------
+// Output tile BA x BB (Na x Nb); reduction over the expert's rows, 64 at a
+// time; both operands are [64 rows][cols] LDS tiles read with the transpose
+// load.  MFMA A operand = B-tile (output columns nb, contiguous in C), MFMA B
+// operand = A-tile (output rows na).
+template <typename TR, int BA, int BB>
+__global__ __launch_bounds__(kThreads, 1) void wgrad_kernel(const uint16_t* __restrict__ A,
+                                                           const uint16_t* __restrict__ B, uint16_t* __restrict__ C,
+                                                           const int* __restrict__ row_offsets, int E, int Na, int Nb,
+                                                           int* __restrict__ work_counter) {
+  static_assert(BA == 128 && BB == 128, "wgrad loader assumes 128 x 128 tiles");
+  constexpr int MB = BA / 64, NB = BB / 64;
+  constexpr int T_BYTES = kBK * 128 * 2;
+  __shared__ __attribute__((aligned(16))) char smem[2 * 2 * T_BYTES];
+  __shared__ int s_tile;
+  char* lds = smem;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wa = wave >> 1, wb = wave & 1;
+  const int ta_n = (Na + BA - 1) / BA, tb_n = (Nb + BB - 1) / BB;
+  const int per_e = ta_n * tb_n;
+  const int total = E * per_e;
+  const int cc = tid & 15;  // 16-byte chunk within a 128-column row
+
+  while (true) {
+    if (tid == 0) s_tile = atomicAdd(work_counter, 1);
+    __syncthreads();
+    const int t = s_tile;
+    __syncthreads();
+    if (t >= total) break;
+    const int e = t / per_e;
+    const int rem = t - e * per_e;
+    const int a0 = (rem / tb_n) * BA, b0 = (rem % tb_n) * BB;
+    const int rs = row_offsets[e], re = row_offsets[e + 1];
+    const int nk = (re - rs + kBK - 1) / kBK;
+    int ca_col = a0 + cc * 8;
+    ca_col = ca_col < Na ? ca_col : Na - 8;
+    int cb_col = b0 + cc * 8;
+    cb_col = cb_col < Nb ? cb_col : Nb - 8;
+
+    u32x4 ra[4], rb[4];
+    auto gload = [&](int kt) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int r = rs + kt * kBK + (tid >> 4) + 16 * i;
+        const bool ok = r < re;
+        ra[i] = ok ? ld16(A + (int64_t)r * Na + ca_col) : u32x4{0, 0, 0, 0};
+        rb[i] = ok ? ld16(B + (int64_t)r * Nb + cb_col) : u32x4{0, 0, 0, 0};
+      }
+    };
+    auto sstore = [&](int buf) {
+      char* la = lds + buf * 2 * T_BYTES;
+      char* lb = la + T_BYTES;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        lds_write16(la, kr_off<128>((tid >> 4) + 16 * i, cc), ra[i]);
+        lds_write16(lb, kr_off<128>((tid >> 4) + 16 * i, cc), rb[i]);
+      }
+    };
+
+    floatx16 acc[NB][MB];
+#pragma unroll
+    for (int b = 0; b < NB; ++b)
+#pragma unroll
+      for (int a = 0; a < MB; ++a)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) acc[b][a][v] = 0.0f;
+
+    if (nk > 0) {
+      gload(0);
+      sstore(0);
+    }
+    __syncthreads();
+    for (int kt = 0; kt < nk; ++kt) {
+      if (kt + 1 < nk) gload(kt + 1);
+      const char* la = lds + (kt & 1) * 2 * T_BYTES;
+      const char* lb = la + T_BYTES;
+#pragma unroll
+      for (int s = 0; s < kBK / 16; ++s) {
+        u32x4 fb[NB], fa[MB];
+#pragma unroll
+        for (int b = 0; b < NB; ++b) fb[b] = tr_operand<128>(lb, wb * (BB / 2) + b * 32, s, lane);
+#pragma unroll
+        for (int a = 0; a < MB; ++a) fa[a] = tr_operand<128>(la, wa * (BA / 2) + a * 32, s, lane);
+#pragma unroll
+        for (int b = 0; b < NB; ++b)
+#pragma unroll
+          for (int a = 0; a < MB; ++a) acc[b][a] = TR::mfma32(fb[b], fa[a], acc[b][a]);
+      }
+      if (kt + 1 < nk) sstore((kt + 1) & 1);
+      __syncthreads();
+    }
+
+    uint16_t* Ce = C + (int64_t)e * Na * Nb;
+#pragma unroll
+    for (int a = 0; a < MB; ++a) {
+      const int na = a0 + wa * (BA / 2) + a * 32 + (lane & 31);
+      if (na >= Na) continue;
+#pragma unroll
+      for (int b = 0; b < NB; ++b)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const int nb = b0 + wb * (BB / 2) + b * 32 + g * 8 + (lane >> 5) * 4;
+          if (nb < Nb)
+            st8(Ce + (int64_t)na * Nb + nb, pack4<TR>(acc[b][a][g * 4 + 0], acc[b][a][g * 4 + 1],
+                                                     acc[b][a][g * 4 + 2], acc[b][a][g * 4 + 3]));
+        }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Host side
+// ---------------------------------------------------------------------------
+constexpr int kBMMin = 128;  // smallest BM any launch uses (sizes the tile table)
+
+int cu_margin() {
+  static int margin = [] {
+    const char* s = getenv("HRM_MOE_HIP_CU_MARGIN");
+    int v = s ? atoi(s) : 0;
+    return v < 0 ? 0 : v;
+  }();
+  return margin;
+}
+
+// Persistent grid: (CUs - margin) x resident workgroups per CU, rounded down to a multiple of 8.
+template <typename KernelT>
+int persistent_grid(KernelT kernel) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return 8;
+  int cus = 0;
+  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus < 1) cus = 8;
+  int occ = 1;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, kernel, kThreads, 0) != hipSuccess || occ < 1) occ = 1;
+  int g = (cus - cu_margin()) * occ;
+  g = (g / 8) * 8;
+  return g < 8 ? 8 : g;
+}
+
+int check_common(int64_t M, int32_t E, int dtype, const void* ws, size_t ws_bytes) {
+  if (M < 0 || E < 1) return HRM_MOE_ERR_INVALID;
+  if (dtype != HRM_MOE_BF16 && dtype != HRM_MOE_F16) return HRM_MOE_ERR_DTYPE;
+  if (E > kMaxExperts || M >= (int64_t(1) << 31)) return HRM_MOE_ERR_UNSUPPORTED;
+  if (!ws || ws_bytes < gemm_ws_bytes(M, E, kBMMin)) return HRM_MOE_ERR_WORKSPACE;
+  return HRM_MOE_OK;
+}
+
+template <typename TR, int KIND, int BM, int BN>
+int launch_mgemm(const void* A, const int32_t* gather, const void* W, const int64_t* tpe, int64_t M, int N, int K,
+                 int E, void* C, void* workspace, void* stream) {
+  GemmWs w = carve(workspace, M, E, kBMMin);
+  const int max_tiles = (int)((M + BM - 1) / BM + E);
+  HRM_LAUNCH(plan_kernel, dim3(1), dim3(1024), 0, stream, tpe, E, M, BM, w.tiles, max_tiles, w.count, w.row_offsets,
+             w.work_counter);
+  const int tiles_n = KIND == KIND_GATHER_SWIGLU ? (N + BN / 2 - 1) / (BN / 2) : (N + BN - 1) / BN;
+  auto kern = mgemm_kernel<TR, KIND, BM, BN>;
+  static int grid = 0;
+  if (grid == 0) grid = persistent_grid(kern);
+  HRM_LAUNCH(kern, dim3(grid), dim3(kThreads), 0, stream, (const uint16_t*)A, gather, (const uint16_t*)W,
+             (uint16_t*)C, w.tiles, w.count, N, K, tiles_n);
+  return HRM_MOE_OK;
+}
+
+template <int KIND>
+int dispatch_mgemm(int dtype, const void* A, const int32_t* gather, const void* W, const int64_t* tpe, int64_t M,
+                   int N, int K, int E, void* C, void* workspace, void* stream) {
+  // 256-row tiles when the average expert has enough rows to fill them.
+  const bool big = M >= (int64_t)E * 192;
+  if (dtype == HRM_MOE_BF16) {
+    return big ? launch_mgemm<BF16, KIND, 256, 128>(A, gather, W, tpe, M, N, K, E, C, workspace, stream)
+               : launch_mgemm<BF16, KIND, 128, 128>(A, gather, W, tpe, M, N, K, E, C, workspace, stream);
+  }
+  return big ? launch_mgemm<F16, KIND, 256, 128>(A, gather, W, tpe, M, N, K, E, C, workspace, stream)
+             : launch_mgemm<F16, KIND, 128, 128>(A, gather, W, tpe, M, N, K, E, C, workspace, stream);
+}
+
+template <typename TR>
+int launch_wgrad(const void* A, const void* B, const int64_t* tpe, int64_t M, int Na, int Nb, int E, void* C,
+                 void* workspace, void* stream) {
+  GemmWs w = carve(workspace, M, E, kBMMin);
+  const int max_tiles = (int)((M + kBMMin - 1) / kBMMin + E);
+  HRM_LAUNCH(plan_kernel, dim3(1), dim3(1024), 0, stream, tpe, E, M, kBMMin, w.tiles, max_tiles, w.count,
+             w.row_offsets, w.work_counter);
+  auto kern = wgrad_kernel<TR, 128, 128>;
+  static int grid = 0;
+  if (grid == 0) grid = persistent_grid(kern);
+  HRM_LAUNCH(kern, dim3(grid), dim3(kThreads), 0, stream, (const uint16_t*)A, (const uint16_t*)B, (uint16_t*)C,
+             w.row_offsets, E, Na, Nb, w.work_counter);
+  return HRM_MOE_OK;
+}
+
+}  // namespace
+}  // namespace hrm
+
+extern "C" size_t hrm_moe_grouped_gemm_workspace_size(int64_t num_rows, int32_t num_experts) {
+  if (num_rows < 0 || num_experts < 1 || num_experts > hrm::kMaxExperts) return 0;
+  return hrm::gemm_ws_bytes(num_rows, num_experts, hrm::kBMMin);
+}
+
+extern "C" int hrm_moe_grouped_gemm_nt(const void* A, const void* W, const int64_t* tokens_per_expert, int64_t M,
+                                       int64_t N, int64_t K, int32_t num_experts, int dtype, void* C, void* workspace,
+                                       size_t workspace_bytes, void* stream) {
+  int st = hrm::check_common(M, num_experts, dtype, workspace, workspace_bytes);
+  if (st) return st;
+  if (N < 1 || K < 1) return HRM_MOE_ERR_INVALID;
+  if (N % 8 || K % 8 || N >= (1 << 30) || K >= (1 << 30)) return HRM_MOE_ERR_UNSUPPORTED;
+  if (M == 0) return HRM_MOE_OK;
+  if (!A || !W || !tokens_per_expert || !C) return HRM_MOE_ERR_INVALID;
+  return hrm::dispatch_mgemm<hrm::KIND_NT>(dtype, A, nullptr, W, tokens_per_expert, M, (int)N, (int)K, num_experts, C,
+                                           workspace, stream);
+}
+
+extern "C" int hrm_moe_grouped_gemm_nn(const void* A, const void* W, const int64_t* tokens_per_expert, int64_t M,
+                                       int64_t N, int64_t K, int32_t num_experts, int dtype, void* C, void* workspace,
+                                       size_t workspace_bytes, void* stream) {
+  int st = hrm::check_common(M, num_experts, dtype, workspace, workspace_bytes);
+  if (st) return st;
+  if (N < 1 || K < 1) return HRM_MOE_ERR_INVALID;
+  if (N % 8 || K % 8 || N >= (1 << 30) || K >= (1 << 30)) return HRM_MOE_ERR_UNSUPPORTED;
+  if (M == 0) return HRM_MOE_OK;
+  if (!A || !W || !tokens_per_expert || !C) return HRM_MOE_ERR_INVALID;
+  return hrm::dispatch_mgemm<hrm::KIND_NN>(dtype, A, nullptr, W, tokens_per_expert, M, (int)N, (int)K, num_experts, C,
+                                           workspace, stream);
+}
+
+extern "C" int hrm_moe_grouped_gemm_tn(const void* A, const void* B, const int64_t* tokens_per_expert, int64_t M,
+                                       int64_t Na, int64_t Nb, int32_t num_experts, int dtype, void* C,
+                                       void* workspace, size_t workspace_bytes, void* stream) {
+  int st = hrm::check_common(M, num_experts, dtype, workspace, workspace_bytes);
+  if (st) return st;
+  if (Na < 1 || Nb < 1) return HRM_MOE_ERR_INVALID;
+  if (Na % 8 || Nb % 8 || Na >= (1 << 30) || Nb >= (1 << 30)) return HRM_MOE_ERR_UNSUPPORTED;
+  if (!tokens_per_expert || !C || (M > 0 && (!A || !B))) return HRM_MOE_ERR_INVALID;
+  if (dtype == HRM_MOE_BF16)
+    return hrm::launch_wgrad<hrm::BF16>(A, B, tokens_per_expert, M, (int)Na, (int)Nb, num_experts, C, workspace,
+                                        stream);
+  return hrm::launch_wgrad<hrm::F16>(A, B, tokens_per_expert, M, (int)Na, (int)Nb, num_experts, C, workspace, stream);
+}
+
+extern "C" int hrm_moe_gate_up_swiglu(const void* hidden, const int32_t* sorted_token_idx,
+                                      const int64_t* tokens_per_expert, const void* gate_up_weight,
+                                      int64_t num_tokens, int64_t num_rows, int64_t hidden_size, int64_t inter_size,
+                                      int32_t num_experts, int dtype, void* act, void* workspace,
+                                      size_t workspace_bytes, void* stream) {
+  int st = hrm::check_common(num_rows, num_experts, dtype, workspace, workspace_bytes);
+  if (st) return st;
+  if (num_tokens < 0 || hidden_size < 1 || inter_size < 1) return HRM_MOE_ERR_INVALID;
+  if (hidden_size % 8 || inter_size % 8 || hidden_size >= (1 << 30) || inter_size >= (1 << 29))
+    return HRM_MOE_ERR_UNSUPPORTED;
+  if (num_rows == 0) return HRM_MOE_OK;
+  if (num_tokens == 0) return HRM_MOE_ERR_INVALID;  // rows need tokens to gather from
+  if (!hidden || !sorted_token_idx || !tokens_per_expert || !gate_up_weight || !act) return HRM_MOE_ERR_INVALID;
+  return hrm::dispatch_mgemm<hrm::KIND_GATHER_SWIGLU>(dtype, hidden, sorted_token_idx, gate_up_weight,
+                                                      tokens_per_expert, num_rows, (int)inter_size, (int)hidden_size,
+                                                      num_experts, act, workspace, stream);
+}

@@ -1,0 +1,189 @@
+// Dispatch: stable counting sort of the T*k routed slots by expert.
+//
+// Replaces models/layers.py:312-322 of the reference (flat expert ids,
+// repeat_interleave token ids, torch.sort(stable=True), index_select, bincount)
+// with three deterministic kernels and no host synchronisation:
+//   1. rank:    blocks of SB (32..4096) consecutive slots.  Each slot sets its bit in an
+//               LDS bitmask row of its bucket.  A slot's rank in the block is the
+//               popcount of the bucket's bits below it (OR is order-free, so
+//               the ranks do not depend on atomic ordering).
+//   2. scan:    one workgroup turns the per-block bucket counts into bucket
+//               offsets and per-block bases, and writes tokens_per_expert and
+//               expert_offsets.
+//   3. scatter: row = base[block][bucket] + rank; writes sorted_token_idx,
+//               sort_idx and slot_to_row.
+// Buckets are the E experts plus one trailing bucket for ids outside [0, E),
+// whose rows land after every valid row.
+#include "common.h"
+
+namespace hrm {
+namespace {
+
+constexpr int kPermThreads = 256;
+constexpr int kMaxExperts = 1024;
+
+// Slots per rank block: keeps (E+1) * SB / 8 bytes of bitmask (and as much
+// again of prefix counts) under 17 KB each, so a block needs at most 34 KB of LDS.
+inline int slots_per_block(int E) {
+  int sb = 4096;
+  while (sb > 32 && (int64_t)(E + 1) * sb / 8 > 17 * 1024) sb /= 2;
+  return sb;
+}
+
+struct PermWs {
+  int32_t* rank;    // [R]
+  int32_t* counts;  // [nb][E+1]
+  int32_t* base;    // [nb][E+1]
+};
+
+inline size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
+
+inline PermWs carve(void* ws, int64_t R, int nb, int E) {
+  char* p = static_cast<char*>(ws);
+  PermWs w;
+  w.rank = reinterpret_cast<int32_t*>(p);
+  p += align256(sizeof(int32_t) * (size_t)R);
+  w.counts = reinterpret_cast<int32_t*>(p);
+  p += align256(sizeof(int32_t) * (size_t)nb * (E + 1));
+  w.base = reinterpret_cast<int32_t*>(p);
+  return w;
+}
+
+inline size_t ws_bytes(int64_t R, int nb, int E) {
+  const size_t n = align256(sizeof(int32_t) * (size_t)R) + 2 * align256(sizeof(int32_t) * (size_t)nb * (E + 1));
+  return n < 256 ? 256 : n;
+}
+
+__device__ __forceinline__ int bucket_of(int64_t e, int E) { return (e >= 0 && e < E) ? (int)e : E; }
+
+__global__ __launch_bounds__(kPermThreads) void permute_rank_kernel(const int64_t* __restrict__ idx, int64_t R, int E,
+                                                                    int SB, int32_t* __restrict__ rank,
+                                                                    int32_t* __restrict__ counts) {
+  extern __shared__ uint32_t smem[];
+  const int words = SB / 32;
+  const int nbk = E + 1;
+  uint32_t* mask = smem;                            // [nbk][words]
+  uint32_t* pref = smem + (size_t)nbk * words;      // [nbk][words]
+  const int64_t s0 = (int64_t)blockIdx.x * SB;
+  const int per = SB >= kPermThreads ? SB / kPermThreads : 1;  // consecutive slots per thread
+  for (int i = threadIdx.x; i < nbk * words; i += kPermThreads) mask[i] = 0u;
+  __syncthreads();
+  for (int i = 0; i < per; ++i) {
+    const int ls = threadIdx.x * per + i;
+    const int64_t s = s0 + ls;
+    if (ls < SB && s < R) {
+      const int b = bucket_of(idx[s], E);
+      atomicOr(&mask[b * words + (ls >> 5)], 1u << (ls & 31));
+    }
+  }
+  __syncthreads();
+  for (int b = threadIdx.x; b < nbk; b += kPermThreads) {
+    uint32_t run = 0;
+    for (int w = 0; w < words; ++w) {
+      pref[b * words + w] = run;
+      run += __popc(mask[b * words + w]);
+    }
+    counts[(int64_t)blockIdx.x * nbk + b] = (int32_t)run;
+  }
+  __syncthreads();
+  for (int i = 0; i < per; ++i) {
+    const int ls = threadIdx.x * per + i;
+    const int64_t s = s0 + ls;
+    if (ls < SB && s < R) {
+      const int b = bucket_of(idx[s], E);
+      const uint32_t below = mask[b * words + (ls >> 5)] & ((1u << (ls & 31)) - 1u);
+      rank[s] = (int32_t)(pref[b * words + (ls >> 5)] + __popc(below));
+    }
+  }
+}
+
+// One workgroup of 1024 threads; bucket b handled by thread b (E+1 <= 1025, so
+// thread 0 also takes bucket 1024 when E == 1024).
+__global__ __launch_bounds__(1024) void permute_scan_kernel(const int32_t* __restrict__ counts, int nb, int E,
+                                                            int32_t* __restrict__ base,
+                                                            int64_t* __restrict__ tokens_per_expert,
+                                                            int32_t* __restrict__ expert_offsets) {
+  __shared__ int32_t tot[kMaxExperts + 2];
+  __shared__ int32_t off[kMaxExperts + 2];
+  const int nbk = E + 1;
+  for (int b = threadIdx.x; b < nbk; b += blockDim.x) {
+    int32_t t = 0;
+    for (int j = 0; j < nb; ++j) t += counts[(int64_t)j * nbk + b];
+    tot[b] = t;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    int32_t run = 0;
+    for (int b = 0; b < nbk; ++b) {
+      off[b] = run;
+      run += tot[b];
+    }
+    off[nbk] = run;
+  }
+  __syncthreads();
+  for (int b = threadIdx.x; b < nbk; b += blockDim.x) {
+    int32_t run = off[b];
+    for (int j = 0; j < nb; ++j) {
+      base[(int64_t)j * nbk + b] = run;
+      run += counts[(int64_t)j * nbk + b];
+    }
+    if (b < E) tokens_per_expert[b] = (int64_t)tot[b];
+    if (b <= E) expert_offsets[b] = off[b];  // expert_offsets[E] = start of the dropped rows
+  }
+}
+
+__global__ __launch_bounds__(256) void permute_scatter_kernel(const int64_t* __restrict__ idx, int64_t R, int E, int k,
+                                                              int SB, const int32_t* __restrict__ rank,
+                                                              const int32_t* __restrict__ base,
+                                                              int32_t* __restrict__ sorted_token_idx,
+                                                              int64_t* __restrict__ sort_idx,
+                                                              int32_t* __restrict__ slot_to_row) {
+  const int64_t s = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (s >= R) return;
+  const int b = bucket_of(idx[s], E);
+  const int32_t row = base[(s / SB) * (E + 1) + b] + rank[s];
+  sorted_token_idx[row] = (int32_t)(s / k);
+  if (sort_idx) sort_idx[row] = s;
+  slot_to_row[s] = row;
+}
+
+}  // namespace
+}  // namespace hrm
+
+extern "C" size_t hrm_moe_permute_workspace_size(int64_t num_tokens, int32_t num_experts, int32_t top_k) {
+  if (num_tokens < 0 || num_experts < 1 || num_experts > hrm::kMaxExperts || top_k < 1) return 0;
+  const int64_t R = num_tokens * top_k;
+  const int sb = hrm::slots_per_block(num_experts);
+  const int nb = (int)((R + sb - 1) / sb);
+  return hrm::ws_bytes(R, nb, num_experts);
+}
+
+extern "C" int hrm_moe_permute(const int64_t* topk_idx, int64_t num_tokens, int32_t num_experts, int32_t top_k,
+                               int64_t* tokens_per_expert, int32_t* expert_offsets, int32_t* sorted_token_idx,
+                               int64_t* sort_idx, int32_t* slot_to_row, void* workspace, size_t workspace_bytes,
+                               void* stream) {
+  if (num_tokens < 0 || num_experts < 1 || top_k < 1) return HRM_MOE_ERR_INVALID;
+  if (num_experts > hrm::kMaxExperts) return HRM_MOE_ERR_UNSUPPORTED;
+  const int64_t R = num_tokens * top_k;
+  if (R >= (int64_t(1) << 31)) return HRM_MOE_ERR_UNSUPPORTED;
+  if (!tokens_per_expert || !expert_offsets) return HRM_MOE_ERR_INVALID;
+  if (R > 0 && (!topk_idx || !sorted_token_idx || !slot_to_row)) return HRM_MOE_ERR_INVALID;
+  const int E = num_experts;
+  const int sb = hrm::slots_per_block(E);
+  const int nb = (int)((R + sb - 1) / sb);
+  const size_t need = hrm::ws_bytes(R, nb, E);
+  if (!workspace || workspace_bytes < need) return HRM_MOE_ERR_WORKSPACE;
+  hrm::PermWs w = hrm::carve(workspace, R, nb, E);
+  if (nb > 0) {
+    const size_t lds = sizeof(uint32_t) * 2 * (size_t)(E + 1) * (sb / 32);
+    HRM_LAUNCH(hrm::permute_rank_kernel, dim3(nb), dim3(hrm::kPermThreads), lds, stream, topk_idx, R, E, sb, w.rank,
+               w.counts);
+  }
+  HRM_LAUNCH(hrm::permute_scan_kernel, dim3(1), dim3(1024), 0, stream, w.counts, nb, E, w.base, tokens_per_expert,
+             expert_offsets);
+  if (R > 0) {
+    HRM_LAUNCH(hrm::permute_scatter_kernel, dim3((unsigned)((R + 255) / 256)), dim3(256), 0, stream, topk_idx, R, E,
+               top_k, sb, w.rank, w.base, sorted_token_idx, sort_idx, slot_to_row);
+  }
+  return HRM_MOE_OK;
+}

@@ -1,0 +1,137 @@
+// Ordering of the k selected experts exactly as torch.topk returns them on ROCm.
+//
+// Shared by the router kernel and a host-compiled checker (hostcheck.cpp), so
+// the CPU test suite exercises the same code the kernel runs.
+//
+// torch.topk (sorted) takes every value above the k-th largest in ascending
+// index order, then values equal to it in ascending index order.  It then
+// orders the k pairs with a descending bitonic network on 32 slots.  That
+// network builds runs of size 2..16, then does one final merge.  A
+// compare-exchange of slots (a, b) in direction d computes
+//   swap = (key[a] > key[b] && valid[a]) || !valid[b]
+// and exchanges when swap == d.  Equal keys are therefore exchanged whenever
+// d is false.  Slots past the first SLOTS (SLOTS = next power of two >= k)
+// hold invalid entries that never move into the first SLOTS, so the network
+// is evaluated on SLOTS slots.  The build stages for sizes above SLOTS, and
+// the final merge, act on those slots as merges with direction false.
+#pragma once
+#include <stdint.h>
+
+#if defined(__HIPCC__) || defined(__HIP__)
+#define HRM_HD __host__ __device__ __forceinline__
+#else
+#define HRM_HD inline
+#endif
+
+namespace hrm {
+
+HRM_HD void bitonic_ce(uint32_t& ka, int& ia, bool& va, uint32_t& kb, int& ib, bool& vb, bool dir) {
+  const bool swap = ((ka > kb) && va) || !vb;
+  if (swap == dir) {
+    const uint32_t tk = ka; ka = kb; kb = tk;
+    const int ti = ia; ia = ib; ib = ti;
+    const bool tv = va; va = vb; vb = tv;
+  }
+}
+
+// Number of direction-false merges over the first SLOTS slots: the build
+// stages of sizes 2*SLOTS..16 plus the final merge.
+template <int SLOTS>
+struct TopkMerges {
+  static constexpr int value = (SLOTS >= 16 ? 0 : (SLOTS >= 8 ? 1 : (SLOTS >= 4 ? 2 : 3))) + 1;
+};
+
+template <int SLOTS>
+HRM_HD void torch_topk_network(uint32_t (&key)[SLOTS], int (&idx)[SLOTS], bool (&valid)[SLOTS]) {
+  constexpr int kBuildMax = SLOTS < 16 ? SLOTS : 16;
+#pragma unroll
+  for (int size = 2; size <= kBuildMax; size *= 2) {
+#pragma unroll
+    for (int stride = size / 2; stride > 0; stride /= 2) {
+#pragma unroll
+      for (int t = 0; t < SLOTS / 2; ++t) {
+        const int a = 2 * t - (t & (stride - 1));
+        bitonic_ce(key[a], idx[a], valid[a], key[a + stride], idx[a + stride], valid[a + stride],
+                   (t & (size / 2)) != 0);
+      }
+    }
+  }
+#pragma unroll
+  for (int m = 0; m < TopkMerges<SLOTS>::value; ++m) {
+#pragma unroll
+    for (int stride = SLOTS / 2; stride > 0; stride /= 2) {
+#pragma unroll
+      for (int t = 0; t < SLOTS / 2; ++t) {
+        const int a = 2 * t - (t & (stride - 1));
+        bitonic_ce(key[a], idx[a], valid[a], key[a + stride], idx[a + stride], valid[a + stride], false);
+      }
+    }
+  }
+}
+
+// From the k selected (key, index) pairs in (key desc, index asc) order
+// (sk, si; entries >= k unused) to torch's output order (gk, gi).  Keys are
+// order-preserving uint32 images of the probabilities.
+template <int SLOTS>
+HRM_HD void torch_topk_order(const uint32_t (&sk)[SLOTS], const int (&si)[SLOTS], int k, uint32_t (&gk)[SLOTS],
+                             int (&gi)[SLOTS]) {
+  uint32_t kth = 0u;
+#pragma unroll
+  for (int r = 0; r < SLOTS; ++r)
+    if (r == k - 1) kth = sk[r];
+  int n_greater = 0;
+#pragma unroll
+  for (int r = 0; r < SLOTS; ++r) n_greater += (r < k && sk[r] > kth) ? 1 : 0;
+  int pos[SLOTS];
+#pragma unroll
+  for (int r = 0; r < SLOTS; ++r) {
+    const bool gr = sk[r] > kth;
+    int p = gr ? 0 : n_greater;
+#pragma unroll
+    for (int u = 0; u < SLOTS; ++u) {
+      if (u < k && ((sk[u] > kth) == gr) && si[u] < si[r]) ++p;
+    }
+    pos[r] = (r < k) ? p : SLOTS;
+  }
+  bool gv[SLOTS];
+#pragma unroll
+  for (int p = 0; p < SLOTS; ++p) {
+    gk[p] = 0u;
+    gi[p] = 0;
+    gv[p] = p < k;
+#pragma unroll
+    for (int r = 0; r < SLOTS; ++r) {
+      if (pos[r] == p) { gk[p] = sk[r]; gi[p] = si[r]; }
+    }
+  }
+  torch_topk_network<SLOTS>(gk, gi, gv);
+}
+
+// Sum of the k weights in the order torch's reduction kernel uses for a
+// [rows, k] tensor reduced over k: block_width = last_pow2(k) threads, thread
+// x accumulating elements x, x + bw, ... in order, then a shfl_down tree.
+template <int SLOTS>
+HRM_HD float torch_row_sum(const float (&w)[SLOTS], int k) {
+  int bw = 1;
+  while (bw * 2 <= k) bw *= 2;
+  float part[SLOTS];
+#pragma unroll
+  for (int x = 0; x < SLOTS; ++x) {
+    float acc = 0.0f;
+#pragma unroll
+    for (int j = 0; j < SLOTS; ++j) {
+      if (j < k && j >= x && ((j - x) % bw) == 0) acc = acc + w[j];
+    }
+    part[x] = acc;
+  }
+#pragma unroll
+  for (int o = 1; o < SLOTS; o *= 2) {
+#pragma unroll
+    for (int x = 0; x + o < SLOTS; x += 2 * o) {
+      if (o < bw) part[x] = part[x] + part[x + o];
+    }
+  }
+  return part[0];
+}
+
+}  // namespace hrm

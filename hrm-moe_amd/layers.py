@@ -1,0 +1,255 @@
+"""Drop-in MoE FFN module for HRM-MoE's ``grouped_triton`` path on gfx950.
+
+``SparseMoESwiGLU`` keeps the constructor, parameter names and shapes, forward
+signature and ``moe_context`` side effects of the reference module
+(models/layers.py:518-634), so configs and checkpoints written for
+``implementation: grouped_triton`` load unchanged.
+
+Forward paths (same arithmetic, same routing bits):
+  * no autograd needed (inference, ``torch.no_grad()``, or nothing requires
+    grad): router kernel -> dispatch kernel -> fused gather + gate_up GEMM +
+    SwiGLU -> down GEMM -> deterministic combine.  Five HIP launches plus the
+    gate GEMM; no host synchronisation.
+  * autograd needed: the reference's grouped composition
+    (models/layers.py:311-334).  The router, dispatch and both grouped GEMMs
+    (forward, dgrad, wgrad) are the HIP kernels.  The gather, SwiGLU,
+    weighting and index_add_ are torch ops, so autograd covers them.
+"""
+from __future__ import annotations
+
+import math
+from typing import Any, Optional, Sequence
+
+import torch
+import torch.nn.functional as F
+from torch import Tensor, nn
+
+from . import ops
+from .grouped_gemm import hip_grouped_linear
+from .profile import record_moe_profile_phase
+
+
+def trunc_normal_init_(tensor: Tensor, std: float = 1.0) -> Tensor:
+    """The reference's approximate truncated normal (models/common.py:10-13): N(0,1) folded into (-3, 3)
+    by fmod, rescaled so the standard deviation is ``std``."""
+    return tensor.normal_().fmod_(3.0).mul_(1.014762601732121 * std)
+
+
+def unwrap_tensor(value):
+    """Tensor or a wrapper with ``.value`` (models/common.py:26-32)."""
+    return getattr(value, "value", value)
+
+
+class LinearInit(nn.Module):
+    """Bias-free linear with truncated LeCun-normal init (models/layers.py:65-90)."""
+
+    def __init__(self, in_features: int, out_features: int, bias: bool, batch_out_features: Sequence[int] = (),
+                 init_std: Optional[float] = None, **kwargs):
+        super().__init__()
+        self.in_features = in_features
+        if init_std is None:
+            init_std = 1.0 / (in_features ** 0.5)
+        self.weight = nn.Parameter(trunc_normal_init_(
+            torch.empty((math.prod(batch_out_features) * out_features, in_features), **kwargs), std=init_std))
+        self.bias = None
+        if bias:
+            self.bias = nn.Parameter(torch.zeros((math.prod(batch_out_features) * out_features,), **kwargs))
+
+    def forward(self, input: Tensor) -> Tensor:
+        return F.linear(input, self.weight, self.bias)
+
+
+def load_balancing_loss_func(routing_weights: Tensor, selected_experts: Tensor, num_experts: int) -> Tensor:
+    """Qwen-style auxiliary load-balancing loss (models/layers.py:163-170)."""
+    tokens_per_expert = torch.bincount(selected_experts.reshape(-1), minlength=num_experts).to(torch.float32) \
+        / selected_experts.shape[0]
+    router_prob_per_expert = routing_weights.mean(dim=0)
+    return torch.sum(tokens_per_expert * router_prob_per_expert) * num_experts
+
+
+class _RouterTopK(torch.autograd.Function):
+    """Router kernel with the gradient of softmax -> top-k gather -> renormalise -> cast.
+
+    Forward is one HIP launch (models/layers.py:606-610).  Backward is the
+    chain rule of those ops, in torch ops on the device:
+      dv  = dw / c - <dw, v> / c^2 * [s >= 1e-12],  c = max(s, 1e-12), s = sum(v)
+      dp  = dprobs + scatter(idx, dv)
+      dz  = p * (dp - <p, dp>)
+    """
+
+    @staticmethod
+    def forward(ctx, logits: Tensor, top_k: int, norm_topk_prob: bool, out_dtype: torch.dtype):
+        probs, w, idx = ops.router_topk(logits, top_k, norm_topk_prob, out_dtype, want_probs=True)
+        ctx.save_for_backward(probs, idx)
+        ctx.norm = norm_topk_prob
+        ctx.logits_dtype = logits.dtype
+        ctx.mark_non_differentiable(idx)
+        return probs, w, idx
+
+    @staticmethod
+    def backward(ctx, g_probs, g_w, _g_idx):
+        probs, idx = ctx.saved_tensors
+        dp = torch.zeros_like(probs) if g_probs is None else g_probs.float().clone()
+        if g_w is not None:
+            v = probs.gather(1, idx)
+            gw = g_w.float()
+            if ctx.norm:
+                s = v.sum(dim=-1, keepdim=True)
+                c = s.clamp_min(1e-12)
+                dv = gw / c - (gw * v).sum(dim=-1, keepdim=True) / (c * c) * (s >= 1e-12).float()
+            else:
+                dv = gw
+            dp.scatter_add_(1, idx, dv)
+        dz = probs * (dp - (probs * dp).sum(dim=-1, keepdim=True))
+        return dz.to(ctx.logits_dtype), None, None, None
+
+
+class SparseMoEGroupedExperts(nn.Module):
+    """Expert weights and compute (models/layers.py:248-357, grouped branch).
+
+    Parameters: ``gate_up_weight`` [E, 2I, H] (gate rows 0..I-1, up rows
+    I..2I-1) and ``down_weight`` [E, H, I].
+    """
+
+    def __init__(self, hidden_size: int, intermediate_size: int, num_experts: int, backend: str = "hip",
+                 init_std_in=None, init_std_out=None, **kwargs):
+        super().__init__()
+        if num_experts <= 0:
+            raise ValueError(f"num_experts must be positive, got {num_experts}")
+        if backend not in ("hip", "triton"):
+            raise ValueError(f"Unsupported grouped MoE backend: {backend}; this build provides the HIP kernels only")
+        if init_std_in is None:
+            init_std_in = 1.0 / (hidden_size ** 0.5)
+        if init_std_out is None:
+            init_std_out = 1.0 / (intermediate_size ** 0.5)
+        self.num_experts = num_experts
+        self.expert_in_one_shard = num_experts
+        self.backend = "hip"
+        self.gate_up_weight = nn.Parameter(trunc_normal_init_(
+            torch.empty((num_experts, 2 * intermediate_size, hidden_size), **kwargs), std=init_std_in))
+        self.down_weight = nn.Parameter(trunc_normal_init_(
+            torch.empty((num_experts, hidden_size, intermediate_size), **kwargs), std=init_std_out))
+
+    def _needs_autograd(self, hidden_states: Tensor, routing_weights: Tensor) -> bool:
+        return torch.is_grad_enabled() and (hidden_states.requires_grad or routing_weights.requires_grad
+                                            or self.gate_up_weight.requires_grad or self.down_weight.requires_grad)
+
+    def compute(self, hidden_states: Tensor, selected_experts: Tensor, routing_weights: Tensor) -> Tensor:
+        """Expert output [T,H] for tokens routed by ``selected_experts`` / ``routing_weights`` [T,k]."""
+        num_tokens = hidden_states.shape[0]
+        dtype = hidden_states.dtype
+        gate_up_weight = self.gate_up_weight.to(dtype)
+        down_weight = self.down_weight.to(dtype)
+        if num_tokens == 0:
+            return torch.zeros_like(hidden_states)
+        routing_weights = routing_weights.to(dtype)
+
+        if not self._needs_autograd(hidden_states, routing_weights):
+            with record_moe_profile_phase("dispatch"):
+                d = ops.permute(selected_experts, self.num_experts)
+            with record_moe_profile_phase("gate_up_gemm"):
+                act = ops.gate_up_swiglu(hidden_states, d, gate_up_weight)
+            with record_moe_profile_phase("down_gemm"):
+                y = ops.grouped_gemm_nt(act, down_weight, d.tokens_per_expert)
+            with record_moe_profile_phase("combine"):
+                return ops.combine(y, d, routing_weights)
+
+        with record_moe_profile_phase("dispatch"):
+            d = ops.permute(selected_experts, self.num_experts, want_sort_idx=True)
+            sorted_token_idx = d.sorted_token_idx.long()
+            sorted_weights = routing_weights.reshape(-1).index_select(0, d.sort_idx)
+            sorted_hidden_states = hidden_states.index_select(0, sorted_token_idx)
+        with record_moe_profile_phase("gate_up_gemm"):
+            gate_up = hip_grouped_linear(sorted_hidden_states, gate_up_weight, d.tokens_per_expert)
+        with record_moe_profile_phase("activation"):
+            gate, up = gate_up.chunk(2, dim=-1)
+            activated = F.silu(gate) * up
+        with record_moe_profile_phase("down_gemm"):
+            expert_output = hip_grouped_linear(activated, down_weight, d.tokens_per_expert)
+        with record_moe_profile_phase("combine"):
+            expert_output = expert_output * sorted_weights[:, None]
+            out = torch.zeros_like(hidden_states)
+            out.index_add_(0, sorted_token_idx, expert_output.to(dtype))
+        return out
+
+    def forward(self, hidden_states: Tensor, selected_experts: Tensor, routing_weights: Tensor,
+                final_hidden_states: Tensor) -> Tensor:
+        """Adds the expert output into ``final_hidden_states`` and returns it (models/layers.py:285-335)."""
+        if hidden_states.shape[0] == 0:
+            return final_hidden_states
+        out = self.compute(hidden_states, selected_experts, routing_weights)
+        if final_hidden_states.requires_grad or out.requires_grad:
+            return final_hidden_states + out
+        return final_hidden_states.add_(out)
+
+
+class SparseMoESwiGLU(nn.Module):
+    """Routed SwiGLU MoE FFN (models/layers.py:518-634) on the HIP kernels.
+
+    ``implementation`` accepts "grouped_hip" and, so that existing configs keep
+    working, "grouped_triton" (models/layers.py:554-567 with backend triton).
+    The reference's other implementations (origin, shard, grouped,
+    grouped_cutlass, grouped_ep) are not part of this build and raise.
+    """
+
+    IMPLEMENTATIONS = ("grouped_hip", "grouped_triton")
+
+    def __init__(self, hidden_size: int, intermediate_size: int, num_experts: int, top_k: int,
+                 norm_topk_prob: bool, implementation: str = "grouped_hip", expert_in_one_shard: int = 1,
+                 init_std_in=None, init_std_out=None, **kwargs):
+        super().__init__()
+        if num_experts <= 0:
+            raise ValueError(f"num_experts must be positive, got {num_experts}")
+        if top_k <= 0 or top_k > num_experts:
+            raise ValueError(f"top_k must be in [1, num_experts], got top_k={top_k}, num_experts={num_experts}")
+        if expert_in_one_shard <= 0 or num_experts % expert_in_one_shard != 0:
+            raise ValueError(
+                f"expert_in_one_shard must divide num_experts, got "
+                f"expert_in_one_shard={expert_in_one_shard}, num_experts={num_experts}")
+        if implementation not in self.IMPLEMENTATIONS:
+            raise ValueError(f"implementation {implementation!r} is not provided by hrm_moe_amd; "
+                             f"use one of {self.IMPLEMENTATIONS}")
+        self.hidden_size = hidden_size
+        self.num_experts = num_experts
+        self.top_k = top_k
+        self.norm_topk_prob = norm_topk_prob
+        self.implementation = implementation
+        self.expert_in_one_shard = expert_in_one_shard
+        self.gate = LinearInit(hidden_size, num_experts, bias=False, init_std=init_std_in, **kwargs)
+        self.experts = SparseMoEGroupedExperts(hidden_size=hidden_size, intermediate_size=intermediate_size,
+                                               num_experts=num_experts, backend="hip", init_std_in=init_std_in,
+                                               init_std_out=init_std_out, **kwargs)
+
+    def forward(self, x: Tensor, moe_context: Optional[dict[str, Any]] = None, total_seqlen: Optional[Tensor] = None,
+                **_seq_info) -> Tensor:
+        original_shape = x.shape
+        hidden_states = x.reshape(-1, self.hidden_size)
+        want_aux = moe_context is not None and torch.is_grad_enabled()
+
+        with record_moe_profile_phase("router"):
+            router_logits = self.gate(hidden_states)
+            if torch.is_grad_enabled() and router_logits.requires_grad:
+                routing_probs, routing_weights, selected_experts = _RouterTopK.apply(
+                    router_logits, self.top_k, self.norm_topk_prob, hidden_states.dtype)
+            else:
+                routing_probs, routing_weights, selected_experts = ops.router_topk(
+                    router_logits, self.top_k, self.norm_topk_prob, hidden_states.dtype, want_probs=want_aux)
+
+        final_hidden_states = self.experts.compute(hidden_states, selected_experts, routing_weights)
+
+        if want_aux:
+            aux_routing_probs = routing_probs
+            aux_selected_experts = selected_experts
+            if total_seqlen is not None:
+                valid_tokens = int(unwrap_tensor(total_seqlen).item())
+                aux_routing_probs = aux_routing_probs[:valid_tokens]
+                aux_selected_experts = aux_selected_experts[:valid_tokens]
+            with record_moe_profile_phase("aux_metrics"):
+                aux_loss = load_balancing_loss_func(aux_routing_probs, aux_selected_experts, self.num_experts)
+                moe_context.setdefault("aux_losses", []).append(aux_loss)
+                with torch.no_grad():
+                    expert_counts = torch.bincount(aux_selected_experts.reshape(-1),
+                                                   minlength=self.num_experts).to(torch.float32)
+                    moe_context.setdefault("expert_counts", []).append(expert_counts)
+
+        return final_hidden_states.reshape(original_shape)

@@ -1,0 +1,228 @@
+"""Device ops: torch tensors in, torch tensors out, one C ABI call each.
+
+Each op checks devices, dtypes and shapes on the host, makes its inputs
+contiguous, allocates outputs and scratch with torch's caching allocator,
+and enqueues the kernel on torch's current stream.  Nothing here reads device
+memory on the host, so no op synchronises.  Every op needs its tensors on a
+ROCm GPU and raises otherwise: there is no CPU path.
+"""
+from __future__ import annotations
+
+from dataclasses import dataclass
+from typing import Optional
+
+import torch
+
+from . import _lib
+
+
+def _require_cuda(*tensors: torch.Tensor) -> torch.device:
+    dev = None
+    for t in tensors:
+        if t is None:
+            continue
+        if not t.is_cuda:
+            raise RuntimeError("hrm_moe_amd kernels need tensors on a ROCm GPU (got a CPU tensor); there is no CPU path")
+        if dev is None:
+            dev = t.device
+        elif t.device != dev:
+            raise RuntimeError(f"tensors on different devices: {dev} and {t.device}")
+    return dev
+
+
+def _workspace(nbytes: int, device: torch.device) -> torch.Tensor:
+    return torch.empty(max(int(nbytes), 256), dtype=torch.uint8, device=device)
+
+
+# ---------------------------------------------------------------------------
+# Router (models/layers.py:606-610)
+# ---------------------------------------------------------------------------
+
+def router_topk(logits: torch.Tensor, top_k: int, norm_topk_prob: bool, weight_dtype: torch.dtype,
+                want_probs: bool = True):
+    """(probs fp32 [T,E] or None, weights [T,k] weight_dtype, idx int64 [T,k]) from router logits [T,E]."""
+    dev = _require_cuda(logits)
+    if logits.dim() != 2:
+        raise ValueError(f"router logits must be [tokens, experts], got {tuple(logits.shape)}")
+    logits = logits.contiguous()
+    t, e = logits.shape
+    probs = torch.empty((t, e), dtype=torch.float32, device=dev) if want_probs else None
+    idx = torch.empty((t, top_k), dtype=torch.int64, device=dev)
+    w = torch.empty((t, top_k), dtype=weight_dtype, device=dev)
+    with torch.cuda.device(dev):
+        st = _lib.load().hrm_moe_router_topk(
+            _lib.ptr(logits), _lib.dtype_code(logits.dtype), t, e, top_k, int(bool(norm_topk_prob)), _lib.ptr(probs),
+            _lib.ptr(idx), _lib.ptr(w), _lib.dtype_code(weight_dtype), _lib.stream_of(dev))
+    _lib.check(st, "router_topk")
+    return probs, w, idx
+
+
+# ---------------------------------------------------------------------------
+# Dispatch (models/layers.py:312-322)
+# ---------------------------------------------------------------------------
+
+@dataclass
+class Dispatch:
+    tokens_per_expert: torch.Tensor  # [E] int64
+    expert_offsets: torch.Tensor     # [E+1] int32
+    sorted_token_idx: torch.Tensor   # [T*k] int32
+    slot_to_row: torch.Tensor        # [T*k] int32
+    sort_idx: Optional[torch.Tensor]  # [T*k] int64 or None
+
+
+def permute(topk_idx: torch.Tensor, num_experts: int, want_sort_idx: bool = False) -> Dispatch:
+    """Stable expert-major order of the routed slots of ``topk_idx`` [T,k] (int64)."""
+    dev = _require_cuda(topk_idx)
+    if topk_idx.dim() != 2:
+        raise ValueError(f"topk_idx must be [tokens, top_k], got {tuple(topk_idx.shape)}")
+    topk_idx = topk_idx.to(torch.int64).contiguous()
+    t, k = topk_idx.shape
+    r = t * k
+    lib = _lib.load()
+    tpe = torch.empty(num_experts, dtype=torch.int64, device=dev)
+    offs = torch.empty(num_experts + 1, dtype=torch.int32, device=dev)
+    sti = torch.empty(r, dtype=torch.int32, device=dev)
+    s2r = torch.empty(r, dtype=torch.int32, device=dev)
+    sidx = torch.empty(r, dtype=torch.int64, device=dev) if want_sort_idx else None
+    ws_bytes = lib.hrm_moe_permute_workspace_size(t, num_experts, k)
+    if ws_bytes == 0:
+        _lib.check(_lib.ERR_UNSUPPORTED if num_experts > 1024 else _lib.ERR_INVALID, "permute")
+    ws = _workspace(ws_bytes, dev)
+    with torch.cuda.device(dev):
+        st = lib.hrm_moe_permute(_lib.ptr(topk_idx), t, num_experts, k, _lib.ptr(tpe), _lib.ptr(offs), _lib.ptr(sti),
+                                 _lib.ptr(sidx), _lib.ptr(s2r), _lib.ptr(ws), ws.numel(), _lib.stream_of(dev))
+    _lib.check(st, "permute")
+    return Dispatch(tpe, offs, sti, s2r, sidx)
+
+
+# ---------------------------------------------------------------------------
+# Grouped GEMMs (models/moe_triton_grouped_gemm.py:358-456)
+# ---------------------------------------------------------------------------
+
+def _gemm_dtype(t: torch.Tensor) -> int:
+    if t.dtype not in (torch.bfloat16, torch.float16):
+        raise TypeError(f"HIP grouped GEMM only supports bf16/fp16, got {t.dtype}")
+    return _lib.dtype_code(t.dtype)
+
+
+def _tpe64(tokens_per_expert: torch.Tensor, device: torch.device) -> torch.Tensor:
+    return tokens_per_expert.to(device=device, dtype=torch.int64).contiguous()
+
+
+def grouped_gemm_nt(a: torch.Tensor, w: torch.Tensor, tokens_per_expert: torch.Tensor) -> torch.Tensor:
+    """C[M,N] = A[M,K] @ W[e][N,K]^T per expert row group."""
+    dev = _require_cuda(a, w)
+    m, k = a.shape
+    e, n, wk = w.shape
+    if wk != k:
+        raise ValueError(f"grouped GEMM K mismatch: input K={k}, weight K={wk}")
+    if w.dtype != a.dtype:
+        raise TypeError(f"grouped GEMM dtype mismatch: input {a.dtype}, weight {w.dtype}")
+    dt = _gemm_dtype(a)
+    a, w = a.contiguous(), w.contiguous()
+    tpe = _tpe64(tokens_per_expert, dev)
+    if tpe.numel() != e:
+        raise ValueError(f"tokens_per_expert has {tpe.numel()} entries for {e} experts")
+    c = a.new_empty((m, n))
+    lib = _lib.load()
+    ws = _workspace(lib.hrm_moe_grouped_gemm_workspace_size(m, e), dev)
+    with torch.cuda.device(dev):
+        st = lib.hrm_moe_grouped_gemm_nt(_lib.ptr(a), _lib.ptr(w), _lib.ptr(tpe), m, n, k, e, dt, _lib.ptr(c),
+                                         _lib.ptr(ws), ws.numel(), _lib.stream_of(dev))
+    _lib.check(st, "grouped_gemm_nt")
+    return c
+
+
+def grouped_gemm_nn(a: torch.Tensor, w: torch.Tensor, tokens_per_expert: torch.Tensor) -> torch.Tensor:
+    """C[M,N] = A[M,K] @ W[e][K,N] per expert row group (dgrad of grouped_gemm_nt)."""
+    dev = _require_cuda(a, w)
+    m, k = a.shape
+    e, wk, n = w.shape
+    if wk != k:
+        raise ValueError(f"grouped GEMM K mismatch: input K={k}, weight K={wk}")
+    if w.dtype != a.dtype:
+        raise TypeError(f"grouped GEMM dtype mismatch: input {a.dtype}, weight {w.dtype}")
+    dt = _gemm_dtype(a)
+    a, w = a.contiguous(), w.contiguous()
+    tpe = _tpe64(tokens_per_expert, dev)
+    if tpe.numel() != e:
+        raise ValueError(f"tokens_per_expert has {tpe.numel()} entries for {e} experts")
+    c = a.new_empty((m, n))
+    lib = _lib.load()
+    ws = _workspace(lib.hrm_moe_grouped_gemm_workspace_size(m, e), dev)
+    with torch.cuda.device(dev):
+        st = lib.hrm_moe_grouped_gemm_nn(_lib.ptr(a), _lib.ptr(w), _lib.ptr(tpe), m, n, k, e, dt, _lib.ptr(c),
+                                         _lib.ptr(ws), ws.numel(), _lib.stream_of(dev))
+    _lib.check(st, "grouped_gemm_nn")
+    return c
+
+
+def grouped_gemm_tn(a: torch.Tensor, b: torch.Tensor, tokens_per_expert: torch.Tensor) -> torch.Tensor:
+    """C[e][Na,Nb] = A[rows_e]^T @ B[rows_e] (wgrad); experts without rows get zeros."""
+    dev = _require_cuda(a, b)
+    m, na = a.shape
+    mb, nb = b.shape
+    if m != mb:
+        raise ValueError(f"grouped wgrad K mismatch: A K={m}, B K={mb}")
+    if b.dtype != a.dtype:
+        raise TypeError(f"grouped wgrad dtype mismatch: {a.dtype} vs {b.dtype}")
+    dt = _gemm_dtype(a)
+    a, b = a.contiguous(), b.contiguous()
+    tpe = _tpe64(tokens_per_expert, dev)
+    e = tpe.numel()
+    c = a.new_empty((e, na, nb))
+    lib = _lib.load()
+    ws = _workspace(lib.hrm_moe_grouped_gemm_workspace_size(m, e), dev)
+    with torch.cuda.device(dev):
+        st = lib.hrm_moe_grouped_gemm_tn(_lib.ptr(a), _lib.ptr(b), _lib.ptr(tpe), m, na, nb, e, dt, _lib.ptr(c),
+                                         _lib.ptr(ws), ws.numel(), _lib.stream_of(dev))
+    _lib.check(st, "grouped_gemm_tn")
+    return c
+
+
+# ---------------------------------------------------------------------------
+# Fused expert projections (models/layers.py:318-334)
+# ---------------------------------------------------------------------------
+
+def gate_up_swiglu(hidden: torch.Tensor, dispatch: Dispatch, gate_up_weight: torch.Tensor) -> torch.Tensor:
+    """act[R,I] = silu(h[tok] @ Wg^T) * (h[tok] @ Wu^T) with the row gather fused into the GEMM."""
+    dev = _require_cuda(hidden, gate_up_weight)
+    t, h = hidden.shape
+    e, two_i, wk = gate_up_weight.shape
+    if wk != h or two_i % 2:
+        raise ValueError(f"gate_up_weight {tuple(gate_up_weight.shape)} does not match hidden size {h}")
+    if gate_up_weight.dtype != hidden.dtype:
+        raise TypeError(f"dtype mismatch: hidden {hidden.dtype}, weight {gate_up_weight.dtype}")
+    dt = _gemm_dtype(hidden)
+    inter = two_i // 2
+    hidden, gate_up_weight = hidden.contiguous(), gate_up_weight.contiguous()
+    r = dispatch.sorted_token_idx.numel()
+    act = hidden.new_empty((r, inter))
+    lib = _lib.load()
+    ws = _workspace(lib.hrm_moe_grouped_gemm_workspace_size(r, e), dev)
+    with torch.cuda.device(dev):
+        st = lib.hrm_moe_gate_up_swiglu(_lib.ptr(hidden), _lib.ptr(dispatch.sorted_token_idx),
+                                        _lib.ptr(dispatch.tokens_per_expert), _lib.ptr(gate_up_weight), t, r, h, inter,
+                                        e, dt, _lib.ptr(act), _lib.ptr(ws), ws.numel(), _lib.stream_of(dev))
+    _lib.check(st, "gate_up_swiglu")
+    return act
+
+
+def combine(expert_out: torch.Tensor, dispatch: Dispatch, topk_weight: torch.Tensor) -> torch.Tensor:
+    """out[t] = sum_j round(expert_out[row(t,j)] * w[t,j]) in fp32, rounded once; [T,H]."""
+    dev = _require_cuda(expert_out, topk_weight)
+    t, k = topk_weight.shape
+    r, h = expert_out.shape
+    if r != t * k:
+        raise ValueError(f"expert_out has {r} rows for {t} tokens x top-{k}")
+    if topk_weight.dtype != expert_out.dtype:
+        raise TypeError(f"dtype mismatch: expert_out {expert_out.dtype}, weights {topk_weight.dtype}")
+    expert_out, topk_weight = expert_out.contiguous(), topk_weight.contiguous()
+    e = dispatch.tokens_per_expert.numel()
+    out = expert_out.new_empty((t, h))
+    with torch.cuda.device(dev):
+        st = _lib.load().hrm_moe_combine(_lib.ptr(expert_out), _lib.ptr(dispatch.slot_to_row), _lib.ptr(topk_weight),
+                                         _lib.ptr(dispatch.expert_offsets), t, k, h, e,
+                                         _lib.dtype_code(expert_out.dtype), _lib.ptr(out), _lib.stream_of(dev))
+    _lib.check(st, "combine")
+    return out

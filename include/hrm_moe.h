@@ -1,0 +1,155 @@
+/*
+ * hrm_moe.h - C ABI of the MI355X (gfx950) kernels for HRM-MoE's routed
+ * SwiGLU MoE FFN (the reference's `grouped_triton` path).
+ *
+ * Conventions
+ *   - Every pointer argument is a device pointer unless stated otherwise.
+ *     Tensors are dense and row-major (C order), with the shapes given in [].
+ *   - `stream` is a hipStream_t (NULL = the default stream).  Every call only
+ *     enqueues work on it: no entry point synchronises with the host,
+ *     allocates memory, or reads device data on the host.
+ *   - dtype codes: HRM_MOE_BF16, HRM_MOE_F16, HRM_MOE_F32.
+ *   - Return value: HRM_MOE_OK (0); a negative HRM_MOE_ERR_* code for an
+ *     argument the entry point rejects before launching anything; or a
+ *     positive hipError_t from the HIP runtime.
+ *   - Scratch memory is passed in by the caller (`workspace`, at least
+ *     `*_workspace_size(...)` bytes, 256-byte aligned).
+ *   - Calls that share a workspace must be ordered on one stream.
+ *
+ * Reference citations are paths relative to the reference repository
+ * (XiaoYee/HRM-MoE).
+ */
+#ifndef HRM_MOE_H_
+#define HRM_MOE_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define HRM_MOE_ABI_VERSION 1
+
+enum hrm_moe_status {
+  HRM_MOE_OK = 0,
+  HRM_MOE_ERR_INVALID = -1,     /* null pointer, negative size, inconsistent sizes */
+  HRM_MOE_ERR_DTYPE = -2,       /* dtype not supported by this entry point */
+  HRM_MOE_ERR_UNSUPPORTED = -3, /* shape outside the kernels' limits (see each entry point) */
+  HRM_MOE_ERR_WORKSPACE = -4    /* workspace null or smaller than required */
+};
+
+enum hrm_moe_dtype { HRM_MOE_BF16 = 0, HRM_MOE_F16 = 1, HRM_MOE_F32 = 2 };
+
+/* ABI version of the loaded library (HRM_MOE_ABI_VERSION). */
+int hrm_moe_abi_version(void);
+
+/* Static description of a status code (never NULL). */
+const char* hrm_moe_status_string(int status);
+
+/*
+ * Router: fp32 softmax over experts, top-k, optional renormalisation, cast.
+ * Replaces models/layers.py:606-610:
+ *   probs = F.softmax(logits, -1, dtype=float32); w, idx = torch.topk(probs, k)
+ *   if norm: w = w / w.sum(-1, keepdim=True).clamp_min(1e-12); w = w.to(dtype)
+ * The softmax reproduces torch's device softmax bit for bit; top-k
+ * reproduces torch.topk's order on ROCm, ties included.
+ *   logits       [T, E] in logits_dtype (bf16, f16 or f32)
+ *   probs        [T, E] fp32, may be NULL (needed only for the aux loss)
+ *   topk_idx     [T, k] int64
+ *   topk_weight  [T, k] in weight_dtype
+ * Limits: 1 <= E <= 128, 1 <= k <= min(E, 32).
+ */
+int hrm_moe_router_topk(const void* logits, int logits_dtype, int64_t num_tokens, int32_t num_experts,
+                        int32_t top_k, int32_t norm_topk_prob, float* probs, int64_t* topk_idx,
+                        void* topk_weight, int weight_dtype, void* stream);
+
+/*
+ * Dispatch: stable counting sort of the T*k routed slots by expert.
+ * Replaces models/layers.py:312-322 (flatten, repeat_interleave,
+ * torch.sort(stable=True), index_select of token ids, torch.bincount):
+ *   tokens_per_expert [E]    int64  bincount(topk_idx, minlength=E)
+ *   expert_offsets    [E+1]  int32  exclusive cumsum of tokens_per_expert
+ *   sorted_token_idx  [T*k]  int32  token of each expert-contiguous row
+ *   sort_idx          [T*k]  int64  slot t*k+j of each row (torch.sort's indices); may be NULL
+ *   slot_to_row       [T*k]  int32  row of slot t*k+j (inverse permutation)
+ * Rows of one expert are in ascending slot order (a stable sort).  Slots whose
+ * expert id lies outside [0, E) are placed after every valid row (rows
+ * >= expert_offsets[E]) and counted in no expert.
+ * Limits: 1 <= E <= 1024, T*k < 2^31.
+ */
+size_t hrm_moe_permute_workspace_size(int64_t num_tokens, int32_t num_experts, int32_t top_k);
+int hrm_moe_permute(const int64_t* topk_idx, int64_t num_tokens, int32_t num_experts, int32_t top_k,
+                    int64_t* tokens_per_expert, int32_t* expert_offsets, int32_t* sorted_token_idx,
+                    int64_t* sort_idx, int32_t* slot_to_row, void* workspace, size_t workspace_bytes,
+                    void* stream);
+
+/*
+ * Grouped GEMMs over expert-contiguous row groups: rows
+ * [sum(tpe[:e]), sum(tpe[:e+1])) belong to expert e.  tokens_per_expert is
+ * int64 on the device and is never read on the host.  fp32 accumulation,
+ * one rounding to dtype at the store.  dtype: bf16 or f16.  Limits: K and N
+ * multiples of 8, E <= 1024, M < 2^31.  Rows past sum(tpe) are not written.
+ */
+size_t hrm_moe_grouped_gemm_workspace_size(int64_t num_rows, int32_t num_experts);
+
+/* C[M,N] = A[M,K] . W[e][N,K]^T for the rows of expert e.
+ * Replaces moe_triton_grouped_gemm.py:358-417 with trans_b=True
+ * (_repeat_interleave_kernel :263-274, _m_grouped_gemm_bk_kernel :113-184):
+ * the forward of triton_grouped_linear (:461-464, :478-485). */
+int hrm_moe_grouped_gemm_nt(const void* A, const void* W, const int64_t* tokens_per_expert, int64_t M,
+                            int64_t N, int64_t K, int32_t num_experts, int dtype, void* C, void* workspace,
+                            size_t workspace_bytes, void* stream);
+
+/* C[M,N] = A[M,K] . W[e][K,N] for the rows of expert e (dgrad).
+ * Replaces moe_triton_grouped_gemm.py:358-417 with trans_b=False
+ * (_m_grouped_gemm_bn_kernel :187-260), called from the backward at :472. */
+int hrm_moe_grouped_gemm_nn(const void* A, const void* W, const int64_t* tokens_per_expert, int64_t M,
+                            int64_t N, int64_t K, int32_t num_experts, int dtype, void* C, void* workspace,
+                            size_t workspace_bytes, void* stream);
+
+/* C[e][Na,Nb] = A[rows_e]^T . B[rows_e] with A [M,Na], B [M,Nb] (wgrad); an
+ * expert without rows gets zeros.
+ * Replaces _k_grouped_gemm (moe_triton_grouped_gemm.py:420-456) and
+ * _k_grouped_gemm_kernel (:277-347), called from the backward at :474. */
+int hrm_moe_grouped_gemm_tn(const void* A, const void* B, const int64_t* tokens_per_expert, int64_t M,
+                            int64_t Na, int64_t Nb, int32_t num_experts, int dtype, void* C, void* workspace,
+                            size_t workspace_bytes, void* stream);
+
+/*
+ * Fused expert input projection: row gather + gate_up grouped GEMM + SwiGLU.
+ *   act[r, i] = silu(h[tok(r)] . Wgu[e][i]) * (h[tok(r)] . Wgu[e][I+i])
+ * with tok = sorted_token_idx and e the expert owning row r (rows are
+ * grouped by tokens_per_expert, as in the grouped GEMMs).  Rounding follows the reference: gate and up are rounded
+ * to dtype, silu(gate) is rounded, then the product.
+ * Replaces models/layers.py:320 (hidden_states.index_select), :325-326
+ * (triton_grouped_linear on gate_up_weight) and :327-329 (silu(gate) * up).
+ *   hidden [T,H], sorted_token_idx [R] (values in [0,T)), tokens_per_expert [E]
+ *   int64, gate_up_weight [E,2I,H], act [R,I].  Workspace as for the grouped
+ *   GEMMs (hrm_moe_grouped_gemm_workspace_size(R, E)).  dtype bf16 or f16.
+ * Limits: H and I multiples of 8, E <= 1024.
+ */
+int hrm_moe_gate_up_swiglu(const void* hidden, const int32_t* sorted_token_idx, const int64_t* tokens_per_expert,
+                           const void* gate_up_weight, int64_t num_tokens, int64_t num_rows, int64_t hidden_size,
+                           int64_t inter_size, int32_t num_experts, int dtype, void* act, void* workspace,
+                           size_t workspace_bytes, void* stream);
+
+/*
+ * Weighted combine back to token order.
+ *   out[t] = round( sum over the token's slots j, in ascending row order, of
+ *                   round(expert_out[slot_to_row[t*k+j]] * topk_weight[t,j]) )
+ * with fp32 accumulation, which is what the reference's multiply and bf16
+ * index_add_ compute on the CPU (models/layers.py:333-334).  Slots whose row
+ * is >= expert_offsets[E] (dropped expert ids) contribute nothing.
+ *   expert_out [R,H], topk_weight [T,k], out [T,H]; dtype bf16, f16 or f32.
+ * Limits: H a multiple of 8, 1 <= k <= 32.
+ */
+int hrm_moe_combine(const void* expert_out, const int32_t* slot_to_row, const void* topk_weight,
+                    const int32_t* expert_offsets, int64_t num_tokens, int32_t top_k, int64_t hidden_size,
+                    int32_t num_experts, int dtype, void* out, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* HRM_MOE_H_ */

@@ -1,0 +1,44 @@
+// Host build of the router's ordering code (hrm-moe_amd/csrc/topk_order.h),
+// so the CPU tests check the exact functions the kernel runs.
+#include <stdint.h>
+
+#include "topk_order.h"
+
+namespace {
+template <int SLOTS>
+void order_rows(int k, int64_t rows, const uint32_t* sel_keys, const int32_t* sel_idx, int32_t* out_idx,
+                float* out_sum) {
+  for (int64_t r = 0; r < rows; ++r) {
+    uint32_t sk[SLOTS] = {};
+    int si[SLOTS] = {};
+    for (int j = 0; j < k; ++j) {
+      sk[j] = sel_keys[r * k + j];
+      si[j] = sel_idx[r * k + j];
+    }
+    uint32_t gk[SLOTS];
+    int gi[SLOTS];
+    hrm::torch_topk_order<SLOTS>(sk, si, k, gk, gi);
+    float w[SLOTS];
+    for (int j = 0; j < SLOTS; ++j) {
+      union { uint32_t u; float f; } c;
+      c.u = gk[j] - 1u;
+      w[j] = c.f;
+    }
+    for (int j = 0; j < k; ++j) out_idx[r * k + j] = gi[j];
+    out_sum[r] = hrm::torch_row_sum<SLOTS>(w, k);
+  }
+}
+}  // namespace
+
+// sel_keys / sel_idx: [rows, k] selected pairs in (key desc, index asc) order,
+// keys = float bits + 1.  Writes torch's output order and the weight sum.
+extern "C" int topk_order_check(int32_t k, int64_t rows, const uint32_t* sel_keys, const int32_t* sel_idx,
+                                int32_t* out_idx, float* out_sum) {
+  if (k < 1 || k > 32) return -1;
+  if (k <= 2) order_rows<2>(k, rows, sel_keys, sel_idx, out_idx, out_sum);
+  else if (k <= 4) order_rows<4>(k, rows, sel_keys, sel_idx, out_idx, out_sum);
+  else if (k <= 8) order_rows<8>(k, rows, sel_keys, sel_idx, out_idx, out_sum);
+  else if (k <= 16) order_rows<16>(k, rows, sel_keys, sel_idx, out_idx, out_sum);
+  else order_rows<32>(k, rows, sel_keys, sel_idx, out_idx, out_sum);
+  return 0;
+}

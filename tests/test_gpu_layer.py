@@ -1,0 +1,176 @@
+"""The MoE FFN layer on the GPU against the oracle, at every configuration's shape.
+
+Parity bar: routing indices, permutation and expert offsets are bit-exact.
+Layer outputs are within bf16 tolerance of the oracle: max relative error
+max|out - ref| / max|ref| <= 2e-2, and the reference's own gate,
+assert_close(rtol=3e-2, atol=2e-2) (scripts/test_moe_shard_equivalence.py:97-98).
+The mean absolute error is printed.  The oracle starts from the logits of the
+device's gate GEMM, the same call the reference makes on the device.
+"""
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+import hrm_moe_amd
+from hrm_moe_amd import ops
+from oracle import moe_oracle as mo
+from oracle import synth
+
+pytestmark = pytest.mark.gpu
+BF = torch.bfloat16
+
+
+def build_layer(cuda, seed, t, h, e, i, k, bias_std=0.0, dtype=BF):
+    x, wg, wgu, wdn = synth.moe_inputs(seed, t, h, e, i, logit_bias_std=bias_std)
+    layer = hrm_moe_amd.SparseMoESwiGLU(h, i, e, k, True, implementation="grouped_triton").to(cuda, dtype)
+    with torch.no_grad():
+        layer.gate.weight.copy_(torch.from_numpy(wg))
+        layer.experts.gate_up_weight.copy_(torch.from_numpy(wgu))
+        layer.experts.down_weight.copy_(torch.from_numpy(wdn))
+    cpu = [torch.from_numpy(a).to(dtype) for a in (x, wg, wgu, wdn)]
+    return layer, cpu
+
+
+def compare_layer(out, ref, what):
+    o, r = out.detach().float().cpu(), ref.detach().float().cpu()
+    d = (o - r).abs()
+    rel = d.max().item() / r.abs().max().item()
+    print(f"{what}: max rel err {rel:.3e}, mean abs err {d.mean().item():.3e}, max|ref| {r.abs().max().item():.3e}")
+    assert rel <= 2e-2, what
+    torch.testing.assert_close(o, r, rtol=3e-2, atol=2e-2)
+
+
+LAYER_CASES = [
+    # name, seed, T, H, E, I, k, bias
+    ("c1_shape_bf16", 11, 512, 256, 8, 128, 2, 0.0),
+    ("l_64x8_t2048", 12, 2048, 1280, 64, 448, 8, 0.0),
+    ("xl_skew_t2048", 13, 2048, 1536, 64, 512, 8, 1.5),
+    ("xl128_t1024", 14, 1024, 1536, 128, 512, 8, 0.0),
+    ("decode_t1", 15, 1, 1536, 64, 512, 8, 0.0),
+    ("decode_t8", 16, 8, 1536, 64, 512, 8, 0.0),
+    ("decode_t64", 17, 64, 1536, 64, 512, 8, 0.0),
+    ("decode_t256", 18, 256, 1536, 64, 512, 8, 0.0),
+]
+
+
+@pytest.mark.parametrize("name,seed,t,h,e,i,k,bias", LAYER_CASES)
+def test_layer_forward_matches_oracle(cuda, name, seed, t, h, e, i, k, bias):
+    layer, (x, wg, wgu, wdn) = build_layer(cuda, seed, t, h, e, i, k, bias)
+    xg = x.to(cuda)
+    with torch.no_grad():
+        out = layer(xg)
+        logits = F.linear(xg, layer.gate.weight)
+        _, w, idx = ops.router_topk(logits, k, True, BF)
+        d = ops.permute(idx, e, want_sort_idx=True)
+    ref, im = mo.moe_forward(x, wg, wgu, wdn, k, True, intermediates=True, logits=logits.cpu())
+    assert torch.equal(idx.cpu(), im["idx"]), "routing indices"
+    assert np.array_equal(d.sort_idx.cpu().numpy(), im["sort_idx"]), "permutation"
+    assert np.array_equal(d.tokens_per_expert.cpu().numpy(), im["tokens_per_expert"]), "tokens per expert"
+    assert np.array_equal(d.expert_offsets.cpu().numpy(), im["expert_offsets"]), "offsets"
+    wd = (w.float().cpu() - im["weights"].float()).abs().max().item()
+    assert wd <= 2 ** -8, "routing weights beyond one bf16 ulp"
+    compare_layer(out, ref, name)
+
+
+def test_layer_full_l_config(cuda):
+    """L 64x8 at 16384 tokens (the measured configuration), checked at full size."""
+    layer, (x, wg, wgu, wdn) = build_layer(cuda, 2, 16384, 1280, 64, 448, 8)
+    xg = x.to(cuda)
+    with torch.no_grad():
+        out = layer(xg)
+        out2 = layer(xg)
+        logits = F.linear(xg, layer.gate.weight)
+    assert torch.equal(out, out2), "forward is not deterministic"
+    ref, im = mo.moe_forward(x, wg, wgu, wdn, 8, True, intermediates=True, logits=logits.cpu())
+    _, _, idx = ops.router_topk(logits, 8, True, BF)
+    assert torch.equal(idx.cpu(), im["idx"])
+    compare_layer(out, ref, "l_64x8_t16384")
+
+
+def test_layer_intermediates_match_oracle(cuda):
+    """Fused gate_up+SwiGLU and down GEMM outputs, row by row."""
+    t, h, e, i, k = 1024, 1280, 64, 448, 8
+    layer, (x, wg, wgu, wdn) = build_layer(cuda, 3, t, h, e, i, k)
+    xg = x.to(cuda)
+    with torch.no_grad():
+        logits = F.linear(xg, layer.gate.weight)
+        _, w, idx = ops.router_topk(logits, k, True, BF)
+        d = ops.permute(idx, e)
+        act = ops.gate_up_swiglu(xg, d, layer.experts.gate_up_weight)
+        y = ops.grouped_gemm_nt(act, layer.experts.down_weight, d.tokens_per_expert)
+        out = ops.combine(y, d, w)
+    _, im = mo.moe_forward(x, wg, wgu, wdn, k, True, intermediates=True, logits=logits.cpu())
+    for name, got, want in (("act", act, im["act"]), ("expert_out", y, im["expert_out"])):
+        dd = (got.float().cpu() - want.float()).abs()
+        rel = dd.max().item() / want.float().abs().max().item()
+        print(f"{name}: max rel {rel:.2e}")
+        assert rel <= 2e-2, name
+    # the combine, fed the oracle's own expert outputs, reproduces the oracle bit for bit
+    out_from_ref = ops.combine(im["expert_out"].to(cuda), d, w)
+    ref_combine = mo.combine(im["expert_out"], im["sorted_weights"], im["sorted_token_idx"], t)
+    assert torch.equal(out_from_ref.cpu(), ref_combine)
+    assert out.shape == (t, h)
+
+
+def test_module_reshape_and_aux_context(cuda):
+    t, h, e, i, k = 256, 256, 8, 128, 2
+    layer, (x, wg, wgu, wdn) = build_layer(cuda, 4, t, h, e, i, k)
+    ctx = {}
+    xg = x.to(cuda).reshape(4, 64, h)
+    out = layer(xg, moe_context=ctx)
+    assert out.shape == (4, 64, h)
+    with torch.no_grad():
+        logits = F.linear(x.to(cuda), layer.gate.weight).cpu()
+    probs, _, idx = mo.router_topk(logits, k, True, BF)
+    aux = mo.load_balancing_loss(probs, idx, e)
+    assert abs(ctx["aux_losses"][0].item() - aux.item()) < 1e-4
+    assert torch.equal(ctx["expert_counts"][0].cpu(), mo.expert_counts(idx, e))
+    ctx2 = {}
+    layer(xg, moe_context=ctx2, total_seqlen=torch.tensor(100))
+    assert ctx2["expert_counts"][0].sum().item() == 100 * k
+
+
+def _reference_training_loss(x, wg, wgu, wdn, k, idx, grad):
+    """fp32 CPU autograd of the reference composition with the device's routing."""
+    x = x.float().requires_grad_(True)
+    wg = wg.float().requires_grad_(True)
+    wgu = wgu.float().requires_grad_(True)
+    wdn = wdn.float().requires_grad_(True)
+    probs = F.softmax(x @ wg.T, dim=-1)
+    v = probs.gather(1, idx)
+    w = v / v.sum(-1, keepdim=True).clamp_min(1e-12)
+    out = torch.zeros_like(x)
+    for e in range(wg.shape[0]):
+        tok, slot = torch.where(idx == e)
+        if tok.numel() == 0:
+            continue
+        gu = x[tok] @ wgu[e].T
+        g, u = gu.chunk(2, -1)
+        y = (F.silu(g) * u) @ wdn[e].T
+        out = out.index_add(0, tok, y * w[tok, slot, None])
+    aux = mo.load_balancing_loss(probs, idx, wg.shape[0])
+    ((out * grad).sum() + aux).backward()
+    return out, (x.grad, wg.grad, wgu.grad, wdn.grad)
+
+
+def test_training_path_forward_backward(cuda):
+    t, h, e, i, k = 512, 256, 8, 128, 2
+    layer, (x, wg, wgu, wdn) = build_layer(cuda, 6, t, h, e, i, k)
+    grad = torch.from_numpy(synth.normal(61, (t, h))).to(BF)
+    xg = x.to(cuda).requires_grad_(True)
+    ctx = {}
+    out = layer(xg, moe_context=ctx)
+    loss = (out.float() * grad.to(cuda).float()).sum() + torch.stack(ctx["aux_losses"]).sum()
+    loss.backward()
+    with torch.no_grad():
+        fused = layer(x.to(cuda))
+        idx = ops.router_topk(F.linear(x.to(cuda), layer.gate.weight), k, True, BF)[2].cpu()
+    compare_layer(out.detach(), fused, "training vs fused forward")
+    ref_out, ref_grads = _reference_training_loss(x, wg, wgu, wdn, k, idx, grad.float())
+    got = (xg.grad, layer.gate.weight.grad, layer.experts.gate_up_weight.grad, layer.experts.down_weight.grad)
+    for name, g_, r_ in zip(("x", "gate", "gate_up", "down"), got, ref_grads):
+        g_, r_ = g_.float().cpu(), r_.float()
+        rel = (g_ - r_).abs().max().item() / r_.abs().max().item()
+        print(f"grad {name}: max rel err {rel:.3e}")
+        assert rel <= 3e-2, name

@@ -1,0 +1,74 @@
+"""Dispatch kernel parity on the GPU: bit-exact against the oracle and torch's stable sort.
+
+Replaces models/layers.py:312-322.  Checked: tokens_per_expert (bincount),
+expert offsets, the stable permutation (torch.sort(stable=True) indices),
+sorted token ids and the inverse permutation; empty experts, one expert
+taking every slot, a single token, E up to 1024, ids outside [0, E).
+"""
+import numpy as np
+import pytest
+import torch
+
+from hrm_moe_amd import ops
+from oracle import moe_oracle as mo
+
+pytestmark = pytest.mark.gpu
+
+
+def random_routing(seed, t, e, k, skew=0.0):
+    rng = np.random.default_rng(seed)
+    if skew > 0:
+        p = np.exp(rng.normal(0, skew, size=e))
+        p /= p.sum()
+    else:
+        p = None
+    return np.stack([rng.choice(e, size=k, replace=False, p=p) for _ in range(t)]).astype(np.int64)
+
+
+def check(idx_np, e, cuda):
+    idx = torch.from_numpy(idx_np).to(cuda)
+    d = ops.permute(idx, e, want_sort_idx=True)
+    ref = mo.permute(idx_np, e)
+    assert np.array_equal(d.tokens_per_expert.cpu().numpy(), ref["tokens_per_expert"])
+    assert np.array_equal(d.expert_offsets.cpu().numpy(), ref["expert_offsets"])
+    assert np.array_equal(d.sort_idx.cpu().numpy(), ref["sort_idx"])
+    assert np.array_equal(d.sorted_token_idx.cpu().numpy(), ref["sorted_token_idx"])
+    assert np.array_equal(d.slot_to_row.cpu().numpy(), ref["slot_to_row"])
+    # torch's own stable sort and bincount on the device agree
+    se, si = torch.sort(idx.reshape(-1), stable=True)
+    assert torch.equal(si, d.sort_idx)
+    assert torch.equal(torch.bincount(idx.reshape(-1), minlength=e), d.tokens_per_expert)
+
+
+@pytest.mark.parametrize("t,e,k,skew", [(4096, 64, 8, 0.0), (16384, 64, 8, 0.0), (4096, 64, 8, 1.5),
+                                        (32768, 128, 8, 1.5), (512, 8, 2, 0.0), (1, 64, 8, 0.0),
+                                        (100, 1024, 4, 0.0), (3000, 256, 8, 2.5), (7, 3, 3, 0.0)])
+def test_permute_matches_oracle(cuda, t, e, k, skew):
+    check(random_routing(t * 7 + e, t, e, k, skew), e, cuda)
+
+
+def test_permute_all_to_one_expert(cuda):
+    idx = np.zeros((5000, 1), np.int64)
+    idx[:, 0] = 13
+    check(idx, 64, cuda)
+
+
+def test_permute_zero_tokens(cuda):
+    d = ops.permute(torch.zeros((0, 8), dtype=torch.int64, device=cuda), 64)
+    assert d.tokens_per_expert.cpu().tolist() == [0] * 64
+    assert d.expert_offsets.cpu().tolist() == [0] * 65
+
+
+def test_permute_out_of_range_ids_go_last(cuda):
+    rng = np.random.default_rng(3)
+    idx = random_routing(4, 1000, 16, 4)
+    bad = rng.random(idx.shape) < 0.05
+    idx[bad] = np.where(rng.random(bad.sum()) < 0.5, -1, 16)
+    d = ops.permute(torch.from_numpy(idx).to(cuda), 16, want_sort_idx=True)
+    flat = idx.reshape(-1)
+    bucket = np.where((flat >= 0) & (flat < 16), flat, 16)
+    order = np.argsort(bucket, kind="stable")
+    assert np.array_equal(d.sort_idx.cpu().numpy(), order)
+    valid = int((bucket < 16).sum())
+    assert d.expert_offsets.cpu().numpy()[-1] == valid
+    assert d.tokens_per_expert.sum().item() == valid
