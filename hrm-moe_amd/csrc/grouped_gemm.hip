@@ -18,11 +18,14 @@
 //    (BM/2) x (BN/2) as 32x32 MFMA blocks of v_mfma_f32_32x32x16_{bf16,f16}.
 //    Operand roles are swapped (W rows feed the MFMA A operand) so each lane
 //    ends with four consecutive output columns and stores 8 bytes.
-//  * K is consumed 64 at a time through two LDS stages.  Row-major K-contiguous
-//    tiles are stored as [rows][64] with the 16-byte chunk index XORed by
-//    (row & 7).  K-strided tiles (dgrad's W, both wgrad operands) are stored
-//    as [k][cols] and read with ds_read_b64_tr_b16, which transposes 4x16
-//    blocks of 16-bit values inside each 16-lane group.
+//  * K is consumed 64 at a time through a ring of LDS stages.  Row-major
+//    K-contiguous tiles are stored as [rows][64] with a swizzled 16-byte chunk
+//    index (kc_swz).  K-strided tiles (dgrad's W, both wgrad operands) are
+//    stored as [k][cols] (kr_swz) and read with ds_read_b64_tr_b16, which
+//    transposes 4x16 blocks of 16-bit values inside each 16-lane group.
+#include <stdio.h>
+#include <stdlib.h>
+
 #include "common.h"
 
 namespace hrm {
@@ -139,11 +142,19 @@ inline GemmWs carve(void* ws, int64_t M, int E, int bm_min) {
 // ---------------------------------------------------------------------------
 // LDS addressing
 // ---------------------------------------------------------------------------
-// [rows][64] tile, K contiguous: 128 B per row, 16-byte chunk c at (c ^ (row & 7)).
-__device__ __forceinline__ uint32_t kc_off(int row, int chunk) { return uint32_t(row * 128 + ((chunk ^ (row & 7)) << 4)); }
-// [64 k][COLS] tile, columns contiguous: 16-byte chunk c of row k at (c ^ ((k & 3) << 1)).
+// LDS serves 64 four-byte banks (256 bytes) per cycle.  The swizzles below
+// make the MFMA operand reads conflict-free under that model.
+// [rows][64] tile, K contiguous: 128 B per row; 16-byte chunk c of row r sits
+// at chunk c ^ ((r >> 1) & 7).  A ds_read_b128 of 16 consecutive rows at one
+// logical chunk then covers 16 distinct (row parity, chunk) bank groups.
+__device__ __forceinline__ int kc_swz(int row) { return (row >> 1) & 7; }
+__device__ __forceinline__ uint32_t kc_off(int row, int chunk) { return uint32_t(row * 128 + ((chunk ^ kc_swz(row)) << 4)); }
+// [64 k][COLS] tile, columns contiguous: 16-byte chunk c of row k sits at
+// chunk c ^ ((k & 3) << 2).  A transpose read covers 4 rows x 4 chunks per
+// 32 lanes; the XOR spreads the 4 rows over distinct quarters of the bank space.
+__device__ __forceinline__ int kr_swz(int k) { return (k & 3) << 2; }
 template <int COLS>
-__device__ __forceinline__ uint32_t kr_off(int k, int chunk) { return uint32_t(k * (COLS * 2) + ((chunk ^ ((k & 3) << 1)) << 4)); }
+__device__ __forceinline__ uint32_t kr_off(int k, int chunk) { return uint32_t(k * (COLS * 2) + ((chunk ^ kr_swz(k)) << 4)); }
 
 // LDS pointers are plain pointers into __shared__ arrays; the compiler infers
 // the LDS address space.  The transpose load takes an explicit LDS pointer.
@@ -490,6 +501,440 @@ __global__ __launch_bounds__(kThreads, 1) void wgrad_kernel(const uint16_t* __re
 }
 
 // ---------------------------------------------------------------------------
+// DMA-fed kernels: buffer_load ... lds fills a ring of LDS stages directly
+// ---------------------------------------------------------------------------
+// Each buffer_load_dwordx4 ... lds writes the 16 bytes of lane L to
+// LDS[M0 + 16 L], so one wave instruction fills 1 KB of a stage.  Each lane
+// therefore chooses its source address so that the bytes land in the
+// swizzled layouts above:
+//   [rows][64] tiles: 8 rows per instruction, lane L -> row L/8, physical
+//                     chunk L%8, logical chunk (L%8) ^ kc_swz(row)
+//   [64 k][128] tiles: 4 rows per instruction, lane L -> row L/16, physical
+//                     chunk L%16, logical chunk (L%16) ^ kr_swz(row)
+// Loads through a buffer resource return zeros past num_records, which zero-fills
+// the wgrad row tails without branches.  The ring is synchronised with
+// an explicit vmcnt wait plus a bare s_barrier per K step.  A workgroup
+// barrier with a memory fence would drain the loads still in flight for
+// later stages.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
+}
+__device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t r, char* lds_dst, uint32_t voff, uint32_t soff) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (HRM_LDS void*)lds_dst, 16, voff, soff, 0, 0);
+}
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt field is 6 bits");
+  __builtin_amdgcn_s_waitcnt((N & 0xF) | 0x70 | 0xF00 | ((N >> 4) << 14));
+}
+// Barrier that orders LDS use without waiting for outstanding vector memory
+// operations; the empty asm statements keep the compiler from moving memory
+// accesses across it.
+__device__ __forceinline__ void barrier_lds() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+// Wait until at most `ahead` stages of `per` loads each are still in flight.
+template <int PER, int MAX_AHEAD>
+__device__ __forceinline__ void wait_stages(int ahead) {
+  if constexpr (MAX_AHEAD >= 2) {
+    if (ahead >= 2) { wait_vmcnt<2 * PER>(); return; }
+  }
+  if constexpr (MAX_AHEAD >= 1) {
+    if (ahead >= 1) { wait_vmcnt<PER>(); return; }
+  }
+  wait_vmcnt<0>();
+}
+
+// silu(gate) * up with the reference's rounding points (gate, up, silu and the
+// product each rounded to the element type), using the hardware exp2 and
+// reciprocal; it stays within one rounding of torch's expf / IEEE-divide silu.
+template <typename TR>
+__device__ __forceinline__ float swiglu_fast(float g, float u) {
+  const float gr = TR::to_f(TR::from_f(g));
+  const float ur = TR::to_f(TR::from_f(u));
+  const float e = __builtin_amdgcn_exp2f(-gr * 1.4426950408889634f);
+  const float sl = TR::to_f(TR::from_f(gr * __builtin_amdgcn_rcpf(1.0f + e)));
+  return sl * ur;
+}
+
+__device__ __forceinline__ void bstore8(__amdgpu_buffer_rsrc_t r, uint32_t voff, u32x2 v) {
+  __builtin_amdgcn_raw_buffer_store_b64(v, r, voff, 0, 0);
+}
+
+// M-grouped GEMM fed by DMA, persistent, with the K steps of consecutive tiles
+// streamed through one LDS ring: while a tile's last steps compute, the ring
+// already receives the next tile's first steps, and that tile's metadata and
+// gathered row ids were loaded early in the current tile.  Requires K % 64 == 0.
+// Output stores go through a buffer resource covering the tile's rows; lanes
+// with nothing to store get an offset past it, so every wave issues the same
+// stores and no branch is taken.
+template <typename TR, int KIND, int BM, int BN, int STAGES>
+__global__ __launch_bounds__(kThreads, 1) void mgemm_dma_kernel(const uint16_t* __restrict__ A,
+                                                               const int32_t* __restrict__ gather,
+                                                               const uint16_t* __restrict__ W,
+                                                               uint16_t* __restrict__ C,
+                                                               const MTile* __restrict__ tiles,
+                                                               const int* __restrict__ tile_count, int N, int K,
+                                                               int tiles_n, uint32_t a_bytes) {
+  constexpr int MB = BM / 64;
+  constexpr int NB = BN / 64;
+  constexpr int A_BYTES = BM * kBK * 2;
+  constexpr int B_BYTES = BN * kBK * 2;
+  constexpr int STAGE_BYTES = A_BYTES + B_BYTES;
+  constexpr int A_INSTR = BM / 32;                          // per wave: 8 rows each, 4 waves
+  constexpr int NN_RPI = 1024 / (BN * 2);                    // NN: [64 k][BN] rows per 1 KB instruction
+  constexpr int NN_LPR = BN / 8;                             // NN: lanes per row
+  constexpr int B_INSTR = KIND == KIND_NN ? 64 / NN_RPI / 4 : BN / 32;
+  constexpr int PER = A_INSTR + B_INSTR;                     // loads per wave per stage
+  static_assert(BN == 128 || BN == 256, "BN is 128 or 256");
+  static_assert(STAGES >= 2 && STAGES <= 4, "2..4 stages");
+  static_assert(STAGES * STAGE_BYTES <= 160 * 1024, "LDS ring exceeds 160 KB");
+  __shared__ __attribute__((aligned(1024))) char smem[STAGES * STAGE_BYTES];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave >> 1, wn = wave & 1;
+
+  const int total = (*tile_count) * tiles_n;
+  const int xcd = blockIdx.x & 7;
+  const int nloc = gridDim.x >> 3;
+  const int chunk = (total + 7) >> 3;
+  const int64_t w_rows = KIND == KIND_GATHER_SWIGLU ? 2 * (int64_t)N : (KIND == KIND_NN ? (int64_t)K : (int64_t)N);
+  const int64_t w_cols = KIND == KIND_NN ? (int64_t)N : (int64_t)K;
+  const int nk = K / kBK;
+  const __amdgpu_buffer_rsrc_t rA = make_rsrc(A, a_bytes);
+  const int lrow8 = lane >> 3;  // row within an 8-row DMA instruction
+
+  // i-th tile of this workgroup (XCD-contiguous order), or -1
+  auto tile_at = [&](int i) __attribute__((always_inline)) -> int {
+    const int jj = (blockIdx.x >> 3) + i * nloc;
+    if (jj >= chunk) return -1;
+    const int t = xcd * chunk + jj;
+    return t < total ? t : -1;
+  };
+
+  // ---- issue side: the tile whose K steps are being fed into the ring.  The
+  // host keeps STAGES - 1 <= K/64, so it is at most one tile ahead of compute.
+  uint32_t a_off[A_INSTR];
+  uint32_t b_off[B_INSTR];
+  __amdgpu_buffer_rsrc_t rB = make_rsrc(W, 0);
+  int iss_rs = 0, iss_re = 0, iss_n0 = 0;
+  int iss_seq = 0;      // sequence number of the issue-side tile
+  int iss_step = 0;     // next local K step to issue
+  bool iss_valid = false;
+  // metadata prefetched for tile iss_seq + 1
+  int pf_t = -1;
+  MTile pf_m = MTile{0, 0, 0, 0};
+  uint32_t pf_src[A_INSTR];
+#pragma unroll
+  for (int i = 0; i < A_INSTR; ++i) pf_src[i] = 0;
+
+  auto load_src = [&](const MTile& m) __attribute__((always_inline)) {
+#pragma unroll
+    for (int i = 0; i < A_INSTR; ++i) {
+      int r = m.row_start + wave * (BM / 4) + i * 8 + lrow8;
+      r = r < m.row_end ? r : m.row_end - 1;
+      pf_src[i] = KIND == KIND_GATHER_SWIGLU ? (uint32_t)gather[r] : (uint32_t)r;
+    }
+  };
+  auto prefetch = [&](int seq) __attribute__((always_inline)) {
+    pf_t = tile_at(seq);
+    if (pf_t >= 0) {
+      pf_m = tiles[pf_t / tiles_n];
+      load_src(pf_m);
+    }
+  };
+  // builds the issue-side context from the prefetched metadata
+  auto take_prefetched = [&]() __attribute__((always_inline)) {
+    // tile metadata is wave-uniform: keep it in SGPRs so descriptors built from
+    // it need no per-lane (waterfall) handling
+    const int nt = __builtin_amdgcn_readfirstlane(pf_t - (pf_t / tiles_n) * tiles_n);
+    iss_rs = __builtin_amdgcn_readfirstlane(pf_m.row_start);
+    iss_re = __builtin_amdgcn_readfirstlane(pf_m.row_end);
+    const int ex = __builtin_amdgcn_readfirstlane(pf_m.expert);
+    rB = make_rsrc(W + (int64_t)ex * w_rows * w_cols, (uint32_t)(w_rows * w_cols * 2));
+#pragma unroll
+    for (int i = 0; i < A_INSTR; ++i) {
+      const int row = wave * (BM / 4) + i * 8 + lrow8;
+      const int lc = (lane & 7) ^ kc_swz(row);
+      a_off[i] = (pf_src[i] * (uint32_t)K + lc * 8) * 2;
+    }
+    if constexpr (KIND == KIND_NN) {
+      iss_n0 = nt * BN;
+#pragma unroll
+      for (int i = 0; i < B_INSTR; ++i) {
+        const int kr = wave * 16 + i * NN_RPI + lane / NN_LPR;
+        const int lc = (lane % NN_LPR) ^ kr_swz(kr);
+        int col = iss_n0 + lc * 8;
+        col = col < N ? col : N - 8;
+        b_off[i] = ((uint32_t)kr * (uint32_t)N + (uint32_t)col) * 2;
+      }
+    } else if constexpr (KIND == KIND_GATHER_SWIGLU) {
+      iss_n0 = nt * (BN / 2);
+#pragma unroll
+      for (int i = 0; i < B_INSTR; ++i) {
+        const int jr = wave * (BN / 4) + i * 8 + lrow8;
+        const int lc = (lane & 7) ^ kc_swz(jr);
+        int cc = iss_n0 + (jr % (BN / 2));
+        cc = cc < N ? cc : N - 1;
+        const uint32_t wr = jr < BN / 2 ? (uint32_t)cc : (uint32_t)(N + cc);
+        b_off[i] = (wr * (uint32_t)K + lc * 8) * 2;
+      }
+    } else {
+      iss_n0 = nt * BN;
+#pragma unroll
+      for (int i = 0; i < B_INSTR; ++i) {
+        const int jr = wave * (BN / 4) + i * 8 + lrow8;
+        const int lc = (lane & 7) ^ kc_swz(jr);
+        int n = iss_n0 + jr;
+        n = n < N ? n : N - 1;
+        b_off[i] = ((uint32_t)n * (uint32_t)K + lc * 8) * 2;
+      }
+    }
+  };
+
+  int issued = 0;  // global K steps issued so far; step g sits in ring slot g % STAGES
+  auto issue_next = [&]() __attribute__((always_inline)) -> bool {
+    if (iss_step == nk) {
+      if (pf_t < 0) return false;
+      take_prefetched();
+      ++iss_seq;
+      iss_step = 0;
+      prefetch(iss_seq + 1);
+    }
+    char* sa = smem + (issued % STAGES) * STAGE_BYTES;
+    char* sb = sa + A_BYTES;
+    const uint32_t ka = (uint32_t)iss_step * (kBK * 2);
+#pragma unroll
+    for (int i = 0; i < A_INSTR; ++i) dma16(rA, sa + (wave * (BM / 4) + i * 8) * 128, a_off[i], ka);
+    if constexpr (KIND == KIND_NN) {
+      const uint32_t kb = (uint32_t)iss_step * kBK * (uint32_t)N * 2;
+#pragma unroll
+      for (int i = 0; i < B_INSTR; ++i) dma16(rB, sb + (wave * 16 + i * NN_RPI) * (BN * 2), b_off[i], kb);
+    } else {
+#pragma unroll
+      for (int i = 0; i < B_INSTR; ++i) dma16(rB, sb + (wave * (BN / 4) + i * 8) * 128, b_off[i], ka);
+    }
+    ++iss_step;
+    ++issued;
+    return true;
+  };
+
+  // first tile
+  prefetch(0);
+  if (pf_t < 0) return;
+  take_prefetched();
+  iss_valid = true;
+  prefetch(1);
+  (void)iss_valid;
+  int comp_rs = iss_rs, comp_re = iss_re, comp_n0 = iss_n0;
+#pragma unroll
+  for (int s2 = 0; s2 < STAGES - 1; ++s2) issue_next();
+
+  int g0 = 0;  // global index of the computing tile's step 0
+  while (true) {
+    floatx16 acc[NB][MB];
+#pragma unroll
+    for (int b = 0; b < NB; ++b)
+#pragma unroll
+      for (int a = 0; a < MB; ++a)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) acc[b][a][v] = 0.0f;
+
+    for (int kt = 0; kt < nk; ++kt) {
+      const int gs = g0 + kt;
+      wait_stages<PER, STAGES - 2>(min(STAGES - 2, issued - gs - 1));
+      barrier_lds();
+      if (issued == gs + STAGES - 1) issue_next();
+      const char* la = smem + (gs % STAGES) * STAGE_BYTES;
+      const char* lb = la + A_BYTES;
+      u32x4 fw[2][NB], fa[2][MB];
+      auto load_frags = [&](int s, u32x4 (&w)[NB], u32x4 (&x)[MB]) __attribute__((always_inline)) {
+#pragma unroll
+        for (int b = 0; b < NB; ++b) {
+          int r0;
+          if constexpr (KIND == KIND_GATHER_SWIGLU)  // gate blocks, then the matching up blocks
+            r0 = (b < NB / 2 ? 0 : BN / 2) + wn * (BN / 4) + (b % (NB / 2)) * 32;
+          else
+            r0 = wn * (BN / 2) + b * 32;
+          if constexpr (KIND == KIND_NN) w[b] = tr_operand<BN>(lb, r0, s, lane);
+          else w[b] = lds_read16(lb, kc_off(r0 + (lane & 31), s * 2 + (lane >> 5)));
+        }
+#pragma unroll
+        for (int a = 0; a < MB; ++a)
+          x[a] = lds_read16(la, kc_off(wm * (BM / 2) + a * 32 + (lane & 31), s * 2 + (lane >> 5)));
+      };
+      load_frags(0, fw[0], fa[0]);
+#pragma unroll
+      for (int s = 0; s < kBK / 16; ++s) {
+        if (s + 1 < kBK / 16) load_frags(s + 1, fw[(s + 1) & 1], fa[(s + 1) & 1]);
+#pragma unroll
+        for (int b = 0; b < NB; ++b)
+#pragma unroll
+          for (int a = 0; a < MB; ++a) acc[b][a] = TR::mfma32(fw[s & 1][b], fa[s & 1][a], acc[b][a]);
+      }
+    }
+
+    // epilogue: buffer stores over this tile's rows
+    const int c_rs = __builtin_amdgcn_readfirstlane(comp_rs);
+    const int c_rows = __builtin_amdgcn_readfirstlane(comp_re - comp_rs);
+    const __amdgpu_buffer_rsrc_t rC = make_rsrc(C + (int64_t)c_rs * N, (uint32_t)c_rows * (uint32_t)N * 2);
+#pragma unroll
+    for (int a = 0; a < MB; ++a) {
+      const uint32_t ml = (uint32_t)(wm * (BM / 2) + a * 32 + (lane & 31));  // row within the tile
+      if constexpr (KIND == KIND_GATHER_SWIGLU) {
+#pragma unroll
+        for (int b = 0; b < NB / 2; ++b)
+#pragma unroll
+          for (int gq = 0; gq < 4; ++gq) {
+            const int c = comp_n0 + wn * (BN / 4) + b * 32 + gq * 8 + (lane >> 5) * 4;
+            float o[4];
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+              o[q] = swiglu_fast<TR>(acc[b][a][gq * 4 + q], acc[b + NB / 2][a][gq * 4 + q]);
+            const uint32_t voff = c < N ? (ml * (uint32_t)N + (uint32_t)c) * 2 : 0x80000000u;
+            bstore8(rC, voff, pack4<TR>(o[0], o[1], o[2], o[3]));
+          }
+      } else {
+#pragma unroll
+        for (int b = 0; b < NB; ++b)
+#pragma unroll
+          for (int gq = 0; gq < 4; ++gq) {
+            const int c = comp_n0 + wn * (BN / 2) + b * 32 + gq * 8 + (lane >> 5) * 4;
+            const uint32_t voff = c < N ? (ml * (uint32_t)N + (uint32_t)c) * 2 : 0x80000000u;
+            bstore8(rC, voff, pack4<TR>(acc[b][a][gq * 4 + 0], acc[b][a][gq * 4 + 1], acc[b][a][gq * 4 + 2],
+                                        acc[b][a][gq * 4 + 3]));
+          }
+      }
+    }
+
+    g0 += nk;
+    if (issued <= g0) break;  // the ring holds no step of a further tile: this was the last one
+    // the issue side has moved on to the next tile (it runs STAGES - 1 >= 1 steps ahead)
+    comp_rs = iss_rs;
+    comp_re = iss_re;
+    comp_n0 = iss_n0;
+  }
+  // drain: no DMA may still be writing LDS when the workgroup retires
+  wait_vmcnt<0>();
+}
+
+// Wgrad fed by DMA: both operands are [64 rows][128 cols] tiles of the
+// expert's rows; rows past the expert's end read as zeros (buffer bounds).
+template <typename TR, int STAGES>
+__global__ __launch_bounds__(kThreads, 1) void wgrad_dma_kernel(const uint16_t* __restrict__ A,
+                                                               const uint16_t* __restrict__ B,
+                                                               uint16_t* __restrict__ C,
+                                                               const int* __restrict__ row_offsets, int E, int Na,
+                                                               int Nb, int* __restrict__ work_counter) {
+  constexpr int BA = 128, BB = 128;
+  constexpr int MB = BA / 64, NB = BB / 64;
+  constexpr int T_BYTES = kBK * 128 * 2;
+  constexpr int STAGE_BYTES = 2 * T_BYTES;
+  constexpr int PER = 8;  // 4 + 4 loads per wave per stage
+  __shared__ __attribute__((aligned(1024))) char smem[STAGES * STAGE_BYTES];
+  __shared__ int s_tile;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wa = wave >> 1, wb = wave & 1;
+  const int ta_n = (Na + BA - 1) / BA, tb_n = (Nb + BB - 1) / BB;
+  const int per_e = ta_n * tb_n;
+  const int total = E * per_e;
+
+  while (true) {
+    if (tid == 0) s_tile = atomicAdd(work_counter, 1);
+    __syncthreads();
+    const int t = s_tile;
+    __syncthreads();
+    if (t >= total) break;
+    const int e = t / per_e;
+    const int rem = t - e * per_e;
+    const int a0 = (rem / tb_n) * BA, b0 = (rem % tb_n) * BB;
+    const int rs = row_offsets[e], re = row_offsets[e + 1];
+    const int nk = (re - rs + kBK - 1) / kBK;
+    const __amdgpu_buffer_rsrc_t rA = make_rsrc(A + (int64_t)rs * Na, (uint32_t)(re - rs) * (uint32_t)Na * 2);
+    const __amdgpu_buffer_rsrc_t rB = make_rsrc(B + (int64_t)rs * Nb, (uint32_t)(re - rs) * (uint32_t)Nb * 2);
+    uint32_t oa[4], ob[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int kr = wave * 16 + i * 4 + (lane >> 4);
+      const int lc = (lane & 15) ^ kr_swz(kr);
+      int ca = a0 + lc * 8, cb = b0 + lc * 8;
+      ca = ca < Na ? ca : Na - 8;
+      cb = cb < Nb ? cb : Nb - 8;
+      oa[i] = ((uint32_t)kr * (uint32_t)Na + (uint32_t)ca) * 2;
+      ob[i] = ((uint32_t)kr * (uint32_t)Nb + (uint32_t)cb) * 2;
+    }
+    auto issue = [&](int kt, int stage) {
+      char* sa = smem + stage * STAGE_BYTES;
+      char* sb = sa + T_BYTES;
+      const uint32_t sofa = (uint32_t)kt * kBK * (uint32_t)Na * 2;
+      const uint32_t sofb = (uint32_t)kt * kBK * (uint32_t)Nb * 2;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        dma16(rA, sa + (wave * 16 + i * 4) * 256, oa[i], sofa);
+        dma16(rB, sb + (wave * 16 + i * 4) * 256, ob[i], sofb);
+      }
+    };
+
+    floatx16 acc[NB][MB];
+#pragma unroll
+    for (int b = 0; b < NB; ++b)
+#pragma unroll
+      for (int a = 0; a < MB; ++a)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) acc[b][a][v] = 0.0f;
+
+#pragma unroll
+    for (int s = 0; s < STAGES - 1; ++s)
+      if (s < nk) issue(s, s);
+    for (int kt = 0; kt < nk; ++kt) {
+      wait_stages<PER, STAGES - 2>(min(STAGES - 2, nk - 1 - kt));
+      barrier_lds();
+      if (kt + STAGES - 1 < nk) issue(kt + STAGES - 1, (kt + STAGES - 1) % STAGES);
+      const char* la = smem + (kt % STAGES) * STAGE_BYTES;
+      const char* lb = la + T_BYTES;
+      u32x4 fb[2][NB], fa[2][MB];
+      auto load_frags = [&](int s, u32x4 (&xb)[NB], u32x4 (&xa)[MB]) {
+#pragma unroll
+        for (int b = 0; b < NB; ++b) xb[b] = tr_operand<128>(lb, wb * (BB / 2) + b * 32, s, lane);
+#pragma unroll
+        for (int a = 0; a < MB; ++a) xa[a] = tr_operand<128>(la, wa * (BA / 2) + a * 32, s, lane);
+      };
+      load_frags(0, fb[0], fa[0]);
+#pragma unroll
+      for (int s = 0; s < kBK / 16; ++s) {
+        if (s + 1 < kBK / 16) load_frags(s + 1, fb[(s + 1) & 1], fa[(s + 1) & 1]);
+#pragma unroll
+        for (int b = 0; b < NB; ++b)
+#pragma unroll
+          for (int a = 0; a < MB; ++a) acc[b][a] = TR::mfma32(fb[s & 1][b], fa[s & 1][a], acc[b][a]);
+      }
+    }
+    barrier_lds();
+
+    uint16_t* Ce = C + (int64_t)e * Na * Nb;
+#pragma unroll
+    for (int a = 0; a < MB; ++a) {
+      const int na = a0 + wa * (BA / 2) + a * 32 + (lane & 31);
+      if (na >= Na) continue;
+#pragma unroll
+      for (int b = 0; b < NB; ++b)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const int nb = b0 + wb * (BB / 2) + b * 32 + g * 8 + (lane >> 5) * 4;
+          if (nb < Nb)
+            st8(Ce + (int64_t)na * Nb + nb, pack4<TR>(acc[b][a][g * 4 + 0], acc[b][a][g * 4 + 1],
+                                                     acc[b][a][g * 4 + 2], acc[b][a][g * 4 + 3]));
+        }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
 // Host side
 // ---------------------------------------------------------------------------
 constexpr int kBMMin = 128;  // smallest BM any launch uses (sizes the tile table)
@@ -541,17 +986,75 @@ int launch_mgemm(const void* A, const int32_t* gather, const void* W, const int6
   return HRM_MOE_OK;
 }
 
+template <typename TR, int KIND, int BM, int BN, int STAGES>
+int launch_mgemm_dma(const void* A, const int32_t* gather, const void* W, const int64_t* tpe, int64_t M, int N,
+                     int K, int E, int64_t a_rows, void* C, void* workspace, void* stream) {
+  GemmWs w = carve(workspace, M, E, kBMMin);
+  const int max_tiles = (int)((M + BM - 1) / BM + E);
+  HRM_LAUNCH(plan_kernel, dim3(1), dim3(1024), 0, stream, tpe, E, M, BM, w.tiles, max_tiles, w.count, w.row_offsets,
+             w.work_counter);
+  const int tiles_n = KIND == KIND_GATHER_SWIGLU ? (N + BN / 2 - 1) / (BN / 2) : (N + BN - 1) / BN;
+  auto kern = mgemm_dma_kernel<TR, KIND, BM, BN, STAGES>;
+  static int grid = 0;
+  if (grid == 0) grid = persistent_grid(kern);
+  HRM_LAUNCH(kern, dim3(grid), dim3(kThreads), 0, stream, (const uint16_t*)A, gather, (const uint16_t*)W,
+             (uint16_t*)C, w.tiles, w.count, N, K, tiles_n, (uint32_t)(a_rows * K * 2));
+  return HRM_MOE_OK;
+}
+
+// Tile shape and pipeline depth of the DMA kernels.  Default: 128 x 128 tiles
+// with 2 stages (64 KB of LDS, two workgroups per CU).
+// HRM_MOE_GEMM_CFG="<rows>x<cols>x<stages>" (e.g. "256x128x3") overrides it.
+struct MCfg {
+  int bm, bn, stages;
+};
+MCfg mgemm_cfg(int64_t M, int E) {
+  static const char* env = getenv("HRM_MOE_GEMM_CFG");
+  if (env) {
+    int bm = 0, bn = 0, st = 0;
+    if (sscanf(env, "%dx%dx%d", &bm, &bn, &st) == 3) {
+      if ((bm == 256 && bn == 256 && st == 2) || (bm == 256 && bn == 128 && st >= 2 && st <= 3) ||
+          (bm == 128 && bn == 128 && st >= 2 && st <= 4))
+        return {bm, bn, st};
+    }
+  }
+  (void)M;
+  (void)E;
+  return MCfg{128, 128, 2};
+}
+
+template <typename TR, int KIND>
+int dispatch_mgemm_t(const void* A, const int32_t* gather, const void* W, const int64_t* tpe, int64_t M, int N, int K,
+                     int E, int64_t a_rows, void* C, void* workspace, void* stream) {
+  const int64_t w_rows = KIND == KIND_GATHER_SWIGLU ? 2 * (int64_t)N : (KIND == KIND_NN ? (int64_t)K : (int64_t)N);
+  const int64_t w_cols = KIND == KIND_NN ? (int64_t)N : (int64_t)K;
+  const bool dma = K % kBK == 0 && a_rows * K * 2 < (int64_t(1) << 32) && w_rows * w_cols * 2 < (int64_t(1) << 32);
+  if (!dma) {
+    // K not a multiple of 64 (or operands beyond 32-bit buffer offsets): register-staged kernel
+    return M >= (int64_t)E * 192 ? launch_mgemm<TR, KIND, 256, 128>(A, gather, W, tpe, M, N, K, E, C, workspace, stream)
+                                 : launch_mgemm<TR, KIND, 128, 128>(A, gather, W, tpe, M, N, K, E, C, workspace, stream);
+  }
+  MCfg c = mgemm_cfg(M, E);
+  // the ring may run at most one tile ahead: STAGES - 1 <= K / 64
+  if (c.stages - 1 > K / kBK) c.stages = K / kBK + 1;
+#define HRM_MG(BM_, BN_, ST_) \
+  return launch_mgemm_dma<TR, KIND, BM_, BN_, ST_>(A, gather, W, tpe, M, N, K, E, a_rows, C, workspace, stream)
+  if (c.bm == 256 && c.bn == 256) HRM_MG(256, 256, 2);
+  if (c.bm == 256) {
+    if (c.stages == 2) HRM_MG(256, 128, 2);
+    HRM_MG(256, 128, 3);
+  }
+  if (c.stages == 2) HRM_MG(128, 128, 2);
+  if (c.stages == 3) HRM_MG(128, 128, 3);
+  HRM_MG(128, 128, 4);
+#undef HRM_MG
+}
+
 template <int KIND>
 int dispatch_mgemm(int dtype, const void* A, const int32_t* gather, const void* W, const int64_t* tpe, int64_t M,
-                   int N, int K, int E, void* C, void* workspace, void* stream) {
-  // 256-row tiles when the average expert has enough rows to fill them.
-  const bool big = M >= (int64_t)E * 192;
-  if (dtype == HRM_MOE_BF16) {
-    return big ? launch_mgemm<BF16, KIND, 256, 128>(A, gather, W, tpe, M, N, K, E, C, workspace, stream)
-               : launch_mgemm<BF16, KIND, 128, 128>(A, gather, W, tpe, M, N, K, E, C, workspace, stream);
-  }
-  return big ? launch_mgemm<F16, KIND, 256, 128>(A, gather, W, tpe, M, N, K, E, C, workspace, stream)
-             : launch_mgemm<F16, KIND, 128, 128>(A, gather, W, tpe, M, N, K, E, C, workspace, stream);
+                   int N, int K, int E, int64_t a_rows, void* C, void* workspace, void* stream) {
+  if (dtype == HRM_MOE_BF16) return dispatch_mgemm_t<BF16, KIND>(A, gather, W, tpe, M, N, K, E, a_rows, C, workspace, stream);
+  return dispatch_mgemm_t<F16, KIND>(A, gather, W, tpe, M, N, K, E, a_rows, C, workspace, stream);
 }
 
 template <typename TR>
@@ -561,11 +1064,30 @@ int launch_wgrad(const void* A, const void* B, const int64_t* tpe, int64_t M, in
   const int max_tiles = (int)((M + kBMMin - 1) / kBMMin + E);
   HRM_LAUNCH(plan_kernel, dim3(1), dim3(1024), 0, stream, tpe, E, M, kBMMin, w.tiles, max_tiles, w.count,
              w.row_offsets, w.work_counter);
-  auto kern = wgrad_kernel<TR, 128, 128>;
-  static int grid = 0;
-  if (grid == 0) grid = persistent_grid(kern);
-  HRM_LAUNCH(kern, dim3(grid), dim3(kThreads), 0, stream, (const uint16_t*)A, (const uint16_t*)B, (uint16_t*)C,
-             w.row_offsets, E, Na, Nb, w.work_counter);
+  const bool dma = M * (int64_t)Na * 2 < (int64_t(1) << 32) && M * (int64_t)Nb * 2 < (int64_t(1) << 32);
+  if (!dma) {
+    auto kern = wgrad_kernel<TR, 128, 128>;
+    static int grid = 0;
+    if (grid == 0) grid = persistent_grid(kern);
+    HRM_LAUNCH(kern, dim3(grid), dim3(kThreads), 0, stream, (const uint16_t*)A, (const uint16_t*)B, (uint16_t*)C,
+               w.row_offsets, E, Na, Nb, w.work_counter);
+    return HRM_MOE_OK;
+  }
+  static const char* env = getenv("HRM_MOE_WGRAD_STAGES");
+  const int stages = env && atoi(env) == 2 ? 2 : 3;
+  if (stages == 2) {
+    auto kern = wgrad_dma_kernel<TR, 2>;
+    static int grid = 0;
+    if (grid == 0) grid = persistent_grid(kern);
+    HRM_LAUNCH(kern, dim3(grid), dim3(kThreads), 0, stream, (const uint16_t*)A, (const uint16_t*)B, (uint16_t*)C,
+               w.row_offsets, E, Na, Nb, w.work_counter);
+  } else {
+    auto kern = wgrad_dma_kernel<TR, 3>;
+    static int grid = 0;
+    if (grid == 0) grid = persistent_grid(kern);
+    HRM_LAUNCH(kern, dim3(grid), dim3(kThreads), 0, stream, (const uint16_t*)A, (const uint16_t*)B, (uint16_t*)C,
+               w.row_offsets, E, Na, Nb, w.work_counter);
+  }
   return HRM_MOE_OK;
 }
 
@@ -586,8 +1108,8 @@ extern "C" int hrm_moe_grouped_gemm_nt(const void* A, const void* W, const int64
   if (N % 8 || K % 8 || N >= (1 << 30) || K >= (1 << 30)) return HRM_MOE_ERR_UNSUPPORTED;
   if (M == 0) return HRM_MOE_OK;
   if (!A || !W || !tokens_per_expert || !C) return HRM_MOE_ERR_INVALID;
-  return hrm::dispatch_mgemm<hrm::KIND_NT>(dtype, A, nullptr, W, tokens_per_expert, M, (int)N, (int)K, num_experts, C,
-                                           workspace, stream);
+  return hrm::dispatch_mgemm<hrm::KIND_NT>(dtype, A, nullptr, W, tokens_per_expert, M, (int)N, (int)K, num_experts, M,
+                                           C, workspace, stream);
 }
 
 extern "C" int hrm_moe_grouped_gemm_nn(const void* A, const void* W, const int64_t* tokens_per_expert, int64_t M,
@@ -599,8 +1121,8 @@ extern "C" int hrm_moe_grouped_gemm_nn(const void* A, const void* W, const int64
   if (N % 8 || K % 8 || N >= (1 << 30) || K >= (1 << 30)) return HRM_MOE_ERR_UNSUPPORTED;
   if (M == 0) return HRM_MOE_OK;
   if (!A || !W || !tokens_per_expert || !C) return HRM_MOE_ERR_INVALID;
-  return hrm::dispatch_mgemm<hrm::KIND_NN>(dtype, A, nullptr, W, tokens_per_expert, M, (int)N, (int)K, num_experts, C,
-                                           workspace, stream);
+  return hrm::dispatch_mgemm<hrm::KIND_NN>(dtype, A, nullptr, W, tokens_per_expert, M, (int)N, (int)K, num_experts, M,
+                                           C, workspace, stream);
 }
 
 extern "C" int hrm_moe_grouped_gemm_tn(const void* A, const void* B, const int64_t* tokens_per_expert, int64_t M,
@@ -632,5 +1154,5 @@ extern "C" int hrm_moe_gate_up_swiglu(const void* hidden, const int32_t* sorted_
   if (!hidden || !sorted_token_idx || !tokens_per_expert || !gate_up_weight || !act) return HRM_MOE_ERR_INVALID;
   return hrm::dispatch_mgemm<hrm::KIND_GATHER_SWIGLU>(dtype, hidden, sorted_token_idx, gate_up_weight,
                                                       tokens_per_expert, num_rows, (int)inter_size, (int)hidden_size,
-                                                      num_experts, act, workspace, stream);
+                                                      num_experts, num_tokens, act, workspace, stream);
 }

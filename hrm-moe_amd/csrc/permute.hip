@@ -3,7 +3,7 @@
 // Replaces models/layers.py:312-322 of the reference (flat expert ids,
 // repeat_interleave token ids, torch.sort(stable=True), index_select, bincount)
 // with three deterministic kernels and no host synchronisation:
-//   1. rank:    blocks of SB (32..4096) consecutive slots.  Each slot sets its bit in an
+//   1. rank:    blocks of SB (32..512) consecutive slots.  Each slot sets its bit in an
 //               LDS bitmask row of its bucket.  A slot's rank in the block is the
 //               popcount of the bucket's bits below it (OR is order-free, so
 //               the ranks do not depend on atomic ordering).
@@ -24,8 +24,10 @@ constexpr int kMaxExperts = 1024;
 
 // Slots per rank block: keeps (E+1) * SB / 8 bytes of bitmask (and as much
 // again of prefix counts) under 17 KB each, so a block needs at most 34 KB of LDS.
+// Smaller blocks give more of them (parallelism) at the cost of a longer scan.
+// 512 slots (one router block of 64 tokens at top-8) when that fits.
 inline int slots_per_block(int E) {
-  int sb = 4096;
+  int sb = 512;
   while (sb > 32 && (int64_t)(E + 1) * sb / 8 > 17 * 1024) sb /= 2;
   return sb;
 }
@@ -97,38 +99,78 @@ __global__ __launch_bounds__(kPermThreads) void permute_rank_kernel(const int64_
   }
 }
 
-// One workgroup of 1024 threads; bucket b handled by thread b (E+1 <= 1025, so
-// thread 0 also takes bucket 1024 when E == 1024).
+// One workgroup of 1024 threads.  With E + 1 <= 1024 buckets, bucket b's nb
+// block counts are split over G = 1024 / (E+1) threads: each sums a contiguous
+// range of blocks, the G partial sums are scanned in LDS, then each thread
+// writes the bases of its range.  With more buckets (E = 1024) each thread
+// walks whole buckets.
 __global__ __launch_bounds__(1024) void permute_scan_kernel(const int32_t* __restrict__ counts, int nb, int E,
                                                             int32_t* __restrict__ base,
                                                             int64_t* __restrict__ tokens_per_expert,
                                                             int32_t* __restrict__ expert_offsets) {
+  __shared__ int32_t part[1024];
   __shared__ int32_t tot[kMaxExperts + 2];
   __shared__ int32_t off[kMaxExperts + 2];
   const int nbk = E + 1;
-  for (int b = threadIdx.x; b < nbk; b += blockDim.x) {
-    int32_t t = 0;
-    for (int j = 0; j < nb; ++j) t += counts[(int64_t)j * nbk + b];
-    tot[b] = t;
+  const int tid = threadIdx.x;
+  const bool split = nbk <= 1024;
+  const int G = split ? 1024 / nbk : 1;
+  const int per = (nb + G - 1) / G;
+  const int b = tid / G, g = tid % G;
+  const bool on = split && b < nbk;
+  const int j0 = g * per, j1 = min(nb, j0 + per);
+  if (split) {
+    int32_t sum = 0;
+    if (on)
+      for (int j = j0; j < j1; ++j) sum += counts[(int64_t)j * nbk + b];
+    part[tid] = sum;
+    __syncthreads();
+    if (on && g == 0) {
+      int32_t run = 0;
+      for (int u = 0; u < G; ++u) {
+        const int32_t v = part[tid + u];
+        part[tid + u] = run;
+        run += v;
+      }
+      tot[b] = run;
+    }
+  } else {
+    for (int bb = tid; bb < nbk; bb += 1024) {
+      int32_t t = 0;
+      for (int j = 0; j < nb; ++j) t += counts[(int64_t)j * nbk + bb];
+      tot[bb] = t;
+    }
   }
   __syncthreads();
-  if (threadIdx.x == 0) {
+  if (tid == 0) {
     int32_t run = 0;
-    for (int b = 0; b < nbk; ++b) {
-      off[b] = run;
-      run += tot[b];
+    for (int bb = 0; bb < nbk; ++bb) {
+      off[bb] = run;
+      run += tot[bb];
     }
-    off[nbk] = run;
   }
   __syncthreads();
-  for (int b = threadIdx.x; b < nbk; b += blockDim.x) {
-    int32_t run = off[b];
-    for (int j = 0; j < nb; ++j) {
-      base[(int64_t)j * nbk + b] = run;
-      run += counts[(int64_t)j * nbk + b];
+  if (split) {
+    if (on) {
+      int32_t run = off[b] + part[tid];
+      for (int j = j0; j < j1; ++j) {
+        const int32_t c = counts[(int64_t)j * nbk + b];
+        base[(int64_t)j * nbk + b] = run;
+        run += c;
+      }
     }
-    if (b < E) tokens_per_expert[b] = (int64_t)tot[b];
-    if (b <= E) expert_offsets[b] = off[b];  // expert_offsets[E] = start of the dropped rows
+  } else {
+    for (int bb = tid; bb < nbk; bb += 1024) {
+      int32_t run = off[bb];
+      for (int j = 0; j < nb; ++j) {
+        base[(int64_t)j * nbk + bb] = run;
+        run += counts[(int64_t)j * nbk + bb];
+      }
+    }
+  }
+  for (int bb = tid; bb < nbk; bb += 1024) {
+    if (bb < E) tokens_per_expert[bb] = (int64_t)tot[bb];
+    expert_offsets[bb] = off[bb];  // expert_offsets[E] = start of the dropped rows
   }
 }
 

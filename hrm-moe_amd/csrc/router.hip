@@ -43,6 +43,30 @@ __device__ __forceinline__ void store_weight(void* p, int dt, int64_t i, float w
   else reinterpret_cast<float*>(p)[i] = w;
 }
 
+// One selection round over a quad: the largest remaining key, ties to the lower
+// expert index; the winner's key is cleared in the lane that holds it.
+template <int C>
+__device__ __forceinline__ void select_round(uint32_t (&key)[C], int e0, uint32_t& out_key, int& out_idx) {
+  uint32_t bk = 0u;
+  int be = 0x7fffffff;
+#pragma unroll
+  for (int j = 0; j < C; ++j) {
+    if (key[j] > bk) { bk = key[j]; be = e0 + j; }
+  }
+  uint32_t ok = dpp_xor1u(bk);
+  int oe = (int)dpp_xor1u((uint32_t)be);
+  if (ok > bk || (ok == bk && oe < be)) { bk = ok; be = oe; }
+  ok = dpp_xor2u(bk);
+  oe = (int)dpp_xor2u((uint32_t)be);
+  if (ok > bk || (ok == bk && oe < be)) { bk = ok; be = oe; }
+#pragma unroll
+  for (int j = 0; j < C; ++j) {
+    if (e0 + j == be) key[j] = 0u;
+  }
+  out_key = bk;
+  out_idx = be;
+}
+
 template <int NP2, int SLOTS>
 __global__ __launch_bounds__(256) void router_topk_kernel(const void* __restrict__ logits, int ldt, int64_t T, int E,
                                                           int k, int norm, float* __restrict__ probs,
@@ -95,54 +119,66 @@ __global__ __launch_bounds__(256) void router_topk_kernel(const void* __restrict
     key[j] = ok ? (__float_as_uint(p) + 1u) : 0u;  // 0 marks "not selectable"
   }
 
-  // Top-k selection in (value desc, index asc) order.
-  uint32_t sk[SLOTS];
-  int si[SLOTS];
+  // Top-k selection in (value desc, index asc) order: k rounds of a quad-wide
+  // argmax (ties to the lower expert index), each removing its winner.
+  if constexpr (SLOTS <= 8) {
+    uint32_t sk[SLOTS];
+    int si[SLOTS];
 #pragma unroll
-  for (int r = 0; r < SLOTS; ++r) {
-    sk[r] = 0u;
-    si[r] = 0;
-    if (r < k) {
-      uint32_t bk = 0u;
-      int be = 0x7fffffff;
+    for (int r = 0; r < SLOTS; ++r) {
+      sk[r] = 0u;
+      si[r] = 0;
+      if (r < k) select_round<C>(key, e0, sk[r], si[r]);
+    }
+    if (!active) return;
+    uint32_t gk[SLOTS];
+    int gi[SLOTS];
+    torch_topk_order<SLOTS>(sk, si, k, gk, gi);
+    float w[SLOTS];
 #pragma unroll
-      for (int j = 0; j < C; ++j) {
-        if (key[j] > bk) { bk = key[j]; be = e0 + j; }
-      }
-      uint32_t ok_ = dpp_xor1u(bk);
-      int oe = (int)dpp_xor1u((uint32_t)be);
-      if (ok_ > bk || (ok_ == bk && oe < be)) { bk = ok_; be = oe; }
-      ok_ = dpp_xor2u(bk);
-      oe = (int)dpp_xor2u((uint32_t)be);
-      if (ok_ > bk || (ok_ == bk && oe < be)) { bk = ok_; be = oe; }
-      sk[r] = bk;
-      si[r] = be;
+    for (int j = 0; j < SLOTS; ++j) w[j] = __uint_as_float(gk[j] - 1u);
+    if (norm) {
+      float sum = torch_row_sum<SLOTS>(w, k);
+      sum = (sum != sum) ? sum : fmaxf(sum, 1e-12f);
 #pragma unroll
-      for (int j = 0; j < C; ++j) {
-        if (e0 + j == be) key[j] = 0u;
+      for (int j = 0; j < SLOTS; ++j) w[j] = w[j] / sum;
+    }
+#pragma unroll
+    for (int j = 0; j < SLOTS; ++j) {
+      if (j < k && (j & 3) == q) {
+        idx_out[row * k + j] = (int64_t)gi[j];
+        store_weight(w_out, wdt, row * k + j, w[j]);
       }
     }
-  }
-  if (!active) return;
-
-  uint32_t gk[SLOTS];
-  int gi[SLOTS];
-  torch_topk_order<SLOTS>(sk, si, k, gk, gi);
-
-  float w[SLOTS];
-#pragma unroll
-  for (int j = 0; j < SLOTS; ++j) w[j] = __uint_as_float(gk[j] - 1u);
-  if (norm) {
-    float sum = torch_row_sum<SLOTS>(w, k);
-    sum = (sum != sum) ? sum : fmaxf(sum, 1e-12f);
-#pragma unroll
-    for (int j = 0; j < SLOTS; ++j) w[j] = w[j] / sum;
-  }
-#pragma unroll
-  for (int j = 0; j < SLOTS; ++j) {
-    if (j < k && (j & 3) == q) {
-      idx_out[row * k + j] = (int64_t)gi[j];
-      store_weight(w_out, wdt, row * k + j, w[j]);
+  } else {
+    // k > 8: the ordering runs in loop form on this row's LDS arrays (one lane per row).
+    __shared__ uint32_t s_sk[64][SLOTS];
+    __shared__ int s_si[64][SLOTS];
+    __shared__ uint32_t s_gk[64][SLOTS];
+    __shared__ int s_gi[64][SLOTS];
+    __shared__ bool s_gv[64][SLOTS];
+    const int lr = threadIdx.x >> 2;
+    for (int r = 0; r < k; ++r) {
+      uint32_t bk;
+      int be;
+      select_round<C>(key, e0, bk, be);
+      if (q == 0) {
+        s_sk[lr][r] = bk;
+        s_si[lr][r] = be;
+      }
+    }
+    if (!active || q != 0) return;
+    torch_topk_order_mem(s_sk[lr], s_si[lr], k, SLOTS, s_gk[lr], s_gi[lr], s_gv[lr]);
+    float w[SLOTS];
+    for (int j = 0; j < k; ++j) w[j] = __uint_as_float(s_gk[lr][j] - 1u);
+    float sum = 1.0f;
+    if (norm) {
+      sum = torch_row_sum_mem(w, k);
+      sum = (sum != sum) ? sum : fmaxf(sum, 1e-12f);
+    }
+    for (int j = 0; j < k; ++j) {
+      idx_out[row * k + j] = (int64_t)s_gi[lr][j];
+      store_weight(w_out, wdt, row * k + j, norm ? w[j] / sum : w[j]);
     }
   }
 }

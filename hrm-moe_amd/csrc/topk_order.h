@@ -134,4 +134,56 @@ HRM_HD float torch_row_sum(const float (&w)[SLOTS], int k) {
   return part[0];
 }
 
+// Loop form of torch_topk_order + torch_row_sum on caller-provided arrays of
+// `slots` entries (slots = next power of two >= k, 2..32).  The router runs this
+// form for k > 8 on per-row LDS arrays, which keeps the large networks out of
+// registers.
+HRM_HD void torch_topk_order_mem(const uint32_t* sk, const int* si, int k, int slots, uint32_t* gk, int* gi,
+                                 bool* gv) {
+  uint32_t kth = sk[k - 1];
+  int n_greater = 0;
+  for (int r = 0; r < k; ++r) n_greater += sk[r] > kth ? 1 : 0;
+  for (int p = 0; p < slots; ++p) {
+    gk[p] = 0u;
+    gi[p] = 0;
+    gv[p] = p < k;
+  }
+  for (int r = 0; r < k; ++r) {
+    const bool gr = sk[r] > kth;
+    int p = gr ? 0 : n_greater;
+    for (int u = 0; u < k; ++u)
+      if (((sk[u] > kth) == gr) && si[u] < si[r]) ++p;
+    gk[p] = sk[r];
+    gi[p] = si[r];
+  }
+  const int build_max = slots < 16 ? slots : 16;
+  for (int size = 2; size <= build_max; size *= 2)
+    for (int stride = size / 2; stride > 0; stride /= 2)
+      for (int t = 0; t < slots / 2; ++t) {
+        const int a = 2 * t - (t & (stride - 1));
+        bitonic_ce(gk[a], gi[a], gv[a], gk[a + stride], gi[a + stride], gv[a + stride], (t & (size / 2)) != 0);
+      }
+  const int merges = (slots >= 16 ? 0 : (slots >= 8 ? 1 : (slots >= 4 ? 2 : 3))) + 1;
+  for (int m = 0; m < merges; ++m)
+    for (int stride = slots / 2; stride > 0; stride /= 2)
+      for (int t = 0; t < slots / 2; ++t) {
+        const int a = 2 * t - (t & (stride - 1));
+        bitonic_ce(gk[a], gi[a], gv[a], gk[a + stride], gi[a + stride], gv[a + stride], false);
+      }
+}
+
+HRM_HD float torch_row_sum_mem(const float* w, int k) {
+  int bw = 1;
+  while (bw * 2 <= k) bw *= 2;
+  float part[32];
+  for (int x = 0; x < bw; ++x) {
+    float acc = 0.0f;
+    for (int j = x; j < k; j += bw) acc = acc + w[j];
+    part[x] = acc;
+  }
+  for (int o = 1; o < bw; o *= 2)
+    for (int x = 0; x + o < bw; x += 2 * o) part[x] = part[x] + part[x + o];
+  return part[0];
+}
+
 }  // namespace hrm

@@ -30,11 +30,38 @@ void order_rows(int k, int64_t rows, const uint32_t* sel_keys, const int32_t* se
 }
 }  // namespace
 
+void order_rows_mem(int k, int64_t rows, const uint32_t* sel_keys, const int32_t* sel_idx, int32_t* out_idx,
+                    float* out_sum) {
+  int slots = 2;
+  while (slots < k) slots *= 2;
+  for (int64_t r = 0; r < rows; ++r) {
+    uint32_t gk[32];
+    int gi[32];
+    bool gv[32];
+    int si[32];
+    for (int j = 0; j < k; ++j) si[j] = sel_idx[r * k + j];
+    hrm::torch_topk_order_mem(sel_keys + r * k, si, k, slots, gk, gi, gv);
+    float w[32];
+    for (int j = 0; j < k; ++j) {
+      union { uint32_t u; float f; } c;
+      c.u = gk[j] - 1u;
+      w[j] = c.f;
+      out_idx[r * k + j] = gi[j];
+    }
+    out_sum[r] = hrm::torch_row_sum_mem(w, k);
+  }
+}
+
 // sel_keys / sel_idx: [rows, k] selected pairs in (key desc, index asc) order,
-// keys = float bits + 1.  Writes torch's output order and the weight sum.
+// keys = float bits + 1.  Writes torch's output order and the weight sum,
+// using the unrolled register form or (loop_form != 0) the loop form.
 extern "C" int topk_order_check(int32_t k, int64_t rows, const uint32_t* sel_keys, const int32_t* sel_idx,
-                                int32_t* out_idx, float* out_sum) {
+                                int32_t* out_idx, float* out_sum, int32_t loop_form) {
   if (k < 1 || k > 32) return -1;
+  if (loop_form) {
+    order_rows_mem(k, rows, sel_keys, sel_idx, out_idx, out_sum);
+    return 0;
+  }
   if (k <= 2) order_rows<2>(k, rows, sel_keys, sel_idx, out_idx, out_sum);
   else if (k <= 4) order_rows<4>(k, rows, sel_keys, sel_idx, out_idx, out_sum);
   else if (k <= 8) order_rows<8>(k, rows, sel_keys, sel_idx, out_idx, out_sum);

@@ -25,30 +25,34 @@ def checker(tmp_path_factory):
     subprocess.run(["g++", "-O1", "-std=c++17", "-shared", "-fPIC", f"-I{HDR_DIR}", SRC, "-o", out], check=True)
     lib = ctypes.CDLL(out)
     lib.topk_order_check.restype = ctypes.c_int
-    lib.topk_order_check.argtypes = [ctypes.c_int32, ctypes.c_int64] + [ctypes.c_void_p] * 4
+    lib.topk_order_check.argtypes = [ctypes.c_int32, ctypes.c_int64] + [ctypes.c_void_p] * 4 + [ctypes.c_int32]
     return lib
 
 
-def run_checker(lib, vals, k):
+def run_checker(lib, vals, k, loop_form=0):
     t, e = vals.shape
     order = np.lexsort((np.broadcast_to(np.arange(e), (t, e)), -vals), axis=-1)[:, :k]
     keys = (np.take_along_axis(vals, order, 1).view(np.uint32) + 1).astype(np.uint32)
     sel = order.astype(np.int32)
     out_idx = np.zeros((t, k), np.int32)
     out_sum = np.zeros(t, np.float32)
-    rc = lib.topk_order_check(k, t, keys.ctypes.data, sel.ctypes.data, out_idx.ctypes.data, out_sum.ctypes.data)
+    rc = lib.topk_order_check(k, t, keys.ctypes.data, sel.ctypes.data, out_idx.ctypes.data, out_sum.ctypes.data,
+                              loop_form)
     assert rc == 0
     return out_idx.astype(np.int64), out_sum
 
 
+@pytest.mark.parametrize("loop_form", [0, 1])
 @pytest.mark.parametrize("k", list(range(1, 33)))
-def test_ordering_matches_oracle_for_every_k(checker, k):
+def test_ordering_matches_oracle_for_every_k(checker, k, loop_form):
     rng = np.random.default_rng(k)
-    e = 64 if k <= 32 else 128
-    vals = (rng.integers(0, 4, size=(600, e)).astype(np.float32) * 0.125 + 0.0625)
-    got, _ = run_checker(checker, vals, k)
+    vals = (rng.integers(0, 4, size=(600, 64)).astype(np.float32) * 0.125 + 0.0625)
+    got, got_sum = run_checker(checker, vals, k, loop_form)
     _, want = mo.topk_rocm(vals, k)
     assert np.array_equal(got, want)
+    if loop_form:
+        _, reg_sum = run_checker(checker, vals, k, 0)
+        assert np.array_equal(got_sum, reg_sum)
 
 
 def test_ordering_matches_device_fixture(checker):
