@@ -8,11 +8,13 @@ Consecutive steps alternate between weight copies so the 256 MB
 Infinity Cache cannot keep one layer's 220 MB of expert weights.
 
 Printed (one JSON line on stdout): active TFLOP/s of the layer (6*R*H*I per
-step, R = T*k), ms per layer, the roofline of the dominant kernel (fused
-gate_up + SwiGLU GEMM, timed with events on its stream) and the reference's
-eager CPU path timed on the host's cores over a bounded sample.
+step, R = T*k), ms per layer, per-op times inside the timed steps, the
+roofline of the dominant kernel (fused gate_up + SwiGLU GEMM, timed with
+events on its stream during the timed steps) and the reference's eager CPU
+path timed on the host's cores over a bounded sample.
 
-Usage: python bench.py [--steps K] [--warmup W] [--gpus 1] [--workload l64x8|xl_skew|xl128|decode_T]
+Usage: python bench.py [--steps K] [--warmup W] [--gpus 1] [--workload l64x8|xl_skew|xl128]
+       python bench.py --calibrate-copy-mb 512   (a plain copy, for scaling rocprofv3 byte counters)
 """
 from __future__ import annotations
 
@@ -24,7 +26,6 @@ import sys
 import time
 
 import torch
-import torch.nn.functional as F
 
 ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
@@ -61,7 +62,49 @@ def make_layer(hrm, dev, t, h, e, i, k, bias_std, seed):
     return layer, x
 
 
-def time_layers(layers, xs, steps, warmup):
+class OpTimer:
+    """Records HIP events around each call of the named ``hrm_moe_amd.ops`` functions.
+
+    The layer looks its ops up on the module at call time, so wrapping the
+    module attributes times the kernels the layer really launches.  Events go
+    on torch's current stream, the stream every op launches on; with the GPU
+    queue kept full by the timed loop, an event pair brackets exactly that
+    op's kernels.
+    """
+
+    NAMES = ("router_topk", "permute", "gate_up_swiglu", "grouped_gemm_nt", "combine")
+
+    def __init__(self, ops):
+        self.ops = ops
+        self.orig = {n: getattr(ops, n) for n in self.NAMES}
+        self.pairs = {n: [] for n in self.NAMES}
+        self.active = False
+        for n, f in self.orig.items():
+            setattr(ops, n, self._wrap(n, f))
+
+    def _wrap(self, name, fn):
+        def timed(*a, **kw):
+            if not self.active:
+                return fn(*a, **kw)
+            s = torch.cuda.Event(enable_timing=True)
+            e = torch.cuda.Event(enable_timing=True)
+            s.record()
+            r = fn(*a, **kw)
+            e.record()
+            self.pairs[name].append((s, e))
+            return r
+        return timed
+
+    def restore(self):
+        for n, f in self.orig.items():
+            setattr(self.ops, n, f)
+
+    def mean_ms(self):
+        return {n: (statistics.fmean(s.elapsed_time(e) for s, e in v) if v else 0.0)
+                for n, v in self.pairs.items()}
+
+
+def time_layers(layers, xs, steps, warmup, timer):
     with torch.no_grad():
         for s in range(warmup):
             layers[s % len(layers)](xs[s % len(xs)])
@@ -69,43 +112,26 @@ def time_layers(layers, xs, steps, warmup):
         t0 = time.perf_counter()
         start = torch.cuda.Event(enable_timing=True)
         end = torch.cuda.Event(enable_timing=True)
+        timer.active = True
         start.record()
         for s in range(steps):
             layers[s % len(layers)](xs[s % len(xs)])
         end.record()
         torch.cuda.synchronize()
+        timer.active = False
         wall = time.perf_counter() - t0
     return start.elapsed_time(end) / steps, wall
 
 
-def phase_times(hrm, layer, x, reps=10):
-    """Per-kernel averages with events on torch's current stream (the stream every op launches on)."""
-    from hrm_moe_amd import ops
-
-    k, e = layer.top_k, layer.num_experts
-    w_gu, w_dn = layer.experts.gate_up_weight, layer.experts.down_weight
-    names = ["gate_gemm", "router", "dispatch", "gate_up_swiglu", "down_gemm", "combine"]
-    acc = {n: [] for n in names}
-    with torch.no_grad():
-        for _ in range(reps + 2):
-            ev = [torch.cuda.Event(enable_timing=True) for _ in range(len(names) + 1)]
-            ev[0].record()
-            logits = F.linear(x, layer.gate.weight)
-            ev[1].record()
-            _, w, idx = ops.router_topk(logits, k, True, x.dtype, want_probs=False)
-            ev[2].record()
-            d = ops.permute(idx, e)
-            ev[3].record()
-            act = ops.gate_up_swiglu(x, d, w_gu)
-            ev[4].record()
-            y = ops.grouped_gemm_nt(act, w_dn, d.tokens_per_expert)
-            ev[5].record()
-            ops.combine(y, d, w)
-            ev[6].record()
-            torch.cuda.synchronize()
-            for j, n in enumerate(names):
-                acc[n].append(ev[j].elapsed_time(ev[j + 1]))
-    return {n: statistics.median(v[2:]) for n, v in acc.items()}
+def calibrate_copy(mb, reps=5):
+    """A plain device copy of ``mb`` MiB, for scaling rocprofv3's FETCH_SIZE / WRITE_SIZE counters."""
+    n = mb * (1 << 20)
+    src = torch.empty(n, dtype=torch.uint8, device="cuda:0").fill_(1)
+    dst = torch.empty_like(src)
+    for _ in range(reps):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"calibrate_copy_bytes_read": n, "calibrate_copy_bytes_written": n, "reps": reps}), flush=True)
 
 
 def read_traffic(name):
@@ -157,11 +183,15 @@ def main():
     ap.add_argument("--workload", default="l64x8", choices=sorted(WORKLOADS))
     ap.add_argument("--weight-copies", type=int, default=2)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--calibrate-copy-mb", type=int, default=0)
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path (run with --gpus 1)", file=sys.stderr)
         sys.exit(2)
     assert torch.cuda.is_available(), "bench.py needs a ROCm GPU"
+    if args.calibrate_copy_mb:
+        calibrate_copy(args.calibrate_copy_mb)
+        return
 
     import hrm_moe_amd as hrm
 
@@ -174,15 +204,25 @@ def main():
         layer, x = make_layer(hrm, dev, t, h, e, i, k, bias, seed=1234 + c)
         layers.append(layer)
         xs.append(x)
-    ms, wall = time_layers(layers, xs, args.steps, args.warmup)
+    timer = OpTimer(hrm.ops)
+    ms, wall = time_layers(layers, xs, args.steps, args.warmup, timer)
+    timer.restore()
     flops = 6.0 * r * h * i
     tflops = flops / (ms * 1e-3) / 1e12
 
-    phases = phase_times(hrm, layers[0], xs[0])
+    op_ms = timer.mean_ms()
+    phases = {
+        "router": op_ms["router_topk"],
+        "dispatch": op_ms["permute"],
+        "gate_up_swiglu": op_ms["gate_up_swiglu"],
+        "down_gemm": op_ms["grouped_gemm_nt"],
+        "combine": op_ms["combine"],
+    }
+    phases["gate_gemm_and_host_gaps"] = max(0.0, ms - sum(phases.values()))
     gate_up_ms = phases["gate_up_swiglu"]
     gate_up_flops = 4.0 * r * h * i
     achieved = gate_up_flops / (gate_up_ms * 1e-3) / 1e12
-    log("phase medians (ms): " + ", ".join(f"{n} {v:.4f}" for n, v in phases.items()))
+    log("per-op means inside the timed steps (ms): " + ", ".join(f"{n} {v:.4f}" for n, v in phases.items()))
     log(f"layer {ms:.4f} ms ({wall / args.steps * 1e3:.4f} ms wall per step), {tflops:.1f} TFLOP/s active, "
         f"{100 * tflops / PEAK_BF16_TFLOPS:.1f}% of bf16 peak")
 
@@ -209,7 +249,7 @@ def main():
         "pct_bf16_peak": round(100 * tflops / PEAK_BF16_TFLOPS, 2),
         "phase_ms": {n: round(v, 5) for n, v in phases.items()},
         "roofline": {
-            "kernel": "mgemm_kernel<BF16, GATHER_SWIGLU, 256, 128> (fused gather + gate_up GEMM + SwiGLU) + its plan kernel",
+            "kernel": "mgemm_dma_kernel<BF16, GATHER_SWIGLU> (fused gather + gate_up GEMM + SwiGLU) + its plan kernel",
             "bound": "mfma",
             "achieved": round(achieved, 2),
             "peak": PEAK_BF16_TFLOPS,
