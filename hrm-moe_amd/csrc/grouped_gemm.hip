@@ -149,6 +149,16 @@ inline GemmWs carve(void* ws, int64_t M, int E, int bm_min) {
 // logical chunk then covers 16 distinct (row parity, chunk) bank groups.
 __device__ __forceinline__ int kc_swz(int row) { return (row >> 1) & 7; }
 __device__ __forceinline__ uint32_t kc_off(int row, int chunk) { return uint32_t(row * 128 + ((chunk ^ kc_swz(row)) << 4)); }
+// The same layout for K slices of other widths: rows of PITCH bytes (64 or
+// 128), chunk index XOR (row / rows-per-256-bytes) mod chunks-per-row.  Each
+// group of 16 lanes reading one chunk column of 16 consecutive rows then
+// covers 256 contiguous bytes, all 64 banks once.
+template <int PITCH>
+__device__ __forceinline__ int kcp_swz(int row) { return (row / (256 / PITCH)) % (PITCH / 16); }
+template <int PITCH>
+__device__ __forceinline__ uint32_t kcp_off(int row, int chunk) {
+  return uint32_t(row * PITCH + ((chunk ^ kcp_swz<PITCH>(row)) << 4));
+}
 // [64 k][COLS] tile, columns contiguous: 16-byte chunk c of row k sits at
 // chunk c ^ ((k & 3) << 2).  A transpose read covers 4 rows x 4 chunks per
 // 32 lanes; the XOR spreads the 4 rows over distinct quarters of the bank space.
@@ -538,6 +548,10 @@ __device__ __forceinline__ void barrier_lds() {
 // Wait until at most `ahead` stages of `per` loads each are still in flight.
 template <int PER, int MAX_AHEAD>
 __device__ __forceinline__ void wait_stages(int ahead) {
+  static_assert(MAX_AHEAD <= 3 && 3 * PER < 64, "vmcnt range");
+  if constexpr (MAX_AHEAD >= 3) {
+    if (ahead >= 3) { wait_vmcnt<3 * PER>(); return; }
+  }
   if constexpr (MAX_AHEAD >= 2) {
     if (ahead >= 2) { wait_vmcnt<2 * PER>(); return; }
   }
@@ -562,6 +576,9 @@ __device__ __forceinline__ float swiglu_fast(float g, float u) {
 __device__ __forceinline__ void bstore8(__amdgpu_buffer_rsrc_t r, uint32_t voff, u32x2 v) {
   __builtin_amdgcn_raw_buffer_store_b64(v, r, voff, 0, 0);
 }
+__device__ __forceinline__ void bstore16(__amdgpu_buffer_rsrc_t r, uint32_t voff, u32x4 v) {
+  __builtin_amdgcn_raw_buffer_store_b128(v, r, voff, 0, 0);
+}
 
 // M-grouped GEMM fed by DMA, persistent, with the K steps of consecutive tiles
 // streamed through one LDS ring: while a tile's last steps compute, the ring
@@ -570,43 +587,92 @@ __device__ __forceinline__ void bstore8(__amdgpu_buffer_rsrc_t r, uint32_t voff,
 // Output stores go through a buffer resource covering the tile's rows; lanes
 // with nothing to store get an offset past it, so every wave issues the same
 // stores and no branch is taken.
-template <typename TR, int KIND, int BM, int BN, int STAGES>
-__global__ __launch_bounds__(kThreads, 1) void mgemm_dma_kernel(const uint16_t* __restrict__ A,
+template <typename TR, int KIND, int BM, int BN, int STAGES, int NW, int BK>
+__global__ __launch_bounds__(NW * 64, 1) void mgemm_dma_kernel(const uint16_t* __restrict__ A,
                                                                const int32_t* __restrict__ gather,
                                                                const uint16_t* __restrict__ W,
                                                                uint16_t* __restrict__ C,
-                                                               const MTile* __restrict__ tiles,
-                                                               const int* __restrict__ tile_count, int N, int K,
-                                                               int tiles_n, uint32_t a_bytes) {
-  constexpr int MB = BM / 64;
-  constexpr int NB = BN / 64;
-  constexpr int A_BYTES = BM * kBK * 2;
-  constexpr int B_BYTES = BN * kBK * 2;
+                                                               const int64_t* __restrict__ tpe, int E, int M, int N,
+                                                               int K, int tiles_n, uint32_t a_bytes) {
+  constexpr int WGN = NW / 2;                                // waves along N (two along M)
+  constexpr int MB = BM / 64;                                // 32-row blocks per wave
+  constexpr int NB = BN / WGN / 32;                          // 32-column blocks per wave
+  constexpr int PK = BK * 2;                                 // bytes per K-contiguous tile row
+  constexpr int LPRK = BK / 8;                               // DMA lanes per K-contiguous row
+  constexpr int RPIK = 64 / LPRK;                            // K-contiguous rows per 1 KB instruction
+  constexpr int A_BYTES = BM * BK * 2;
+  constexpr int B_BYTES = BN * BK * 2;
   constexpr int STAGE_BYTES = A_BYTES + B_BYTES;
-  constexpr int A_INSTR = BM / 32;                          // per wave: 8 rows each, 4 waves
-  constexpr int NN_RPI = 1024 / (BN * 2);                    // NN: [64 k][BN] rows per 1 KB instruction
+  constexpr int A_ROWS = BM / NW;                            // A rows loaded per wave
+  constexpr int A_INSTR = A_ROWS / RPIK;
+  constexpr int NN_RPI = 1024 / (BN * 2);                    // NN: [BK k][BN] rows per 1 KB instruction
   constexpr int NN_LPR = BN / 8;                             // NN: lanes per row
-  constexpr int B_INSTR = KIND == KIND_NN ? 64 / NN_RPI / 4 : BN / 32;
+  constexpr int NN_KR = BK / NW;                             // NN: k rows loaded per wave
+  constexpr int B_ROWS = BN / NW;                            // NT: B rows loaded per wave
+  constexpr int B_INSTR = KIND == KIND_NN ? NN_KR / NN_RPI : B_ROWS / RPIK;
+  static_assert(BK == 32 || BK == 64, "K step is 32 or 64");
   constexpr int PER = A_INSTR + B_INSTR;                     // loads per wave per stage
+  static_assert(NW == 4 || NW == 8, "4 or 8 waves");
   static_assert(BN == 128 || BN == 256, "BN is 128 or 256");
-  static_assert(STAGES >= 2 && STAGES <= 4, "2..4 stages");
+  static_assert(A_INSTR >= 1 && B_INSTR >= 1 && NB >= 1 && (KIND != KIND_GATHER_SWIGLU || NB % 2 == 0), "tile split");
+  static_assert(STAGES >= 2 && STAGES <= 5, "2..5 stages");
   static_assert(STAGES * STAGE_BYTES <= 160 * 1024, "LDS ring exceeds 160 KB");
   __shared__ __attribute__((aligned(1024))) char smem[STAGES * STAGE_BYTES];
+  extern __shared__ int plan_lds[];  // [3][E]: row start, row end, inclusive M-tile prefix
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int wm = wave >> 1, wn = wave & 1;
+  const int wm = wave / WGN, wn = wave % WGN;
 
-  const int total = (*tile_count) * tiles_n;
+  // M-tile plan from tokens_per_expert, built by wave 0 of every workgroup:
+  // expert e owns rows [s_rs[e], s_re[e]) (prefix sums clamped to M) and
+  // M-tiles [s_tp[e-1], s_tp[e]).
+  int* s_rs = plan_lds;
+  int* s_re = plan_lds + E;
+  int* s_tp = plan_lds + 2 * E;
+  if (wave == 0) {
+    int64_t carry_rows = 0;
+    int carry_t = 0;
+    for (int c = 0; c < E; c += 64) {
+      const int e = c + lane;
+      int64_t n = e < E ? tpe[e] : 0;
+      n = n > 0 ? n : 0;
+      int64_t v = n;
+#pragma unroll
+      for (int o = 1; o < 64; o <<= 1) {
+        const int64_t u = __shfl_up(v, o, 64);
+        if (lane >= o) v += u;
+      }
+      const int64_t end = carry_rows + v;
+      const int rs = (int)(end - n < M ? end - n : M);
+      const int re = (int)(end < M ? end : M);
+      int it = (re - rs + BM - 1) / BM;
+#pragma unroll
+      for (int o = 1; o < 64; o <<= 1) {
+        const int u = __shfl_up(it, o, 64);
+        if (lane >= o) it += u;
+      }
+      if (e < E) {
+        s_rs[e] = rs;
+        s_re[e] = re;
+        s_tp[e] = carry_t + it;
+      }
+      carry_rows += __shfl(v, 63, 64);
+      carry_t += __shfl(it, 63, 64);
+    }
+  }
+  __syncthreads();
+  const int total = s_tp[E - 1] * tiles_n;
   const int xcd = blockIdx.x & 7;
   const int nloc = gridDim.x >> 3;
   const int chunk = (total + 7) >> 3;
   const int64_t w_rows = KIND == KIND_GATHER_SWIGLU ? 2 * (int64_t)N : (KIND == KIND_NN ? (int64_t)K : (int64_t)N);
   const int64_t w_cols = KIND == KIND_NN ? (int64_t)N : (int64_t)K;
-  const int nk = K / kBK;
+  const int nk = K / BK;
   const __amdgpu_buffer_rsrc_t rA = make_rsrc(A, a_bytes);
-  const int lrow8 = lane >> 3;  // row within an 8-row DMA instruction
+  const int lrowk = lane / LPRK;  // row within a DMA instruction
+  const int lchk = lane % LPRK;   // physical 16-byte chunk within that row
 
   // i-th tile of this workgroup (XCD-contiguous order), or -1
   auto tile_at = [&](int i) __attribute__((always_inline)) -> int {
@@ -635,7 +701,7 @@ __global__ __launch_bounds__(kThreads, 1) void mgemm_dma_kernel(const uint16_t* 
   auto load_src = [&](const MTile& m) __attribute__((always_inline)) {
 #pragma unroll
     for (int i = 0; i < A_INSTR; ++i) {
-      int r = m.row_start + wave * (BM / 4) + i * 8 + lrow8;
+      int r = m.row_start + wave * A_ROWS + i * RPIK + lrowk;
       r = r < m.row_end ? r : m.row_end - 1;
       pf_src[i] = KIND == KIND_GATHER_SWIGLU ? (uint32_t)gather[r] : (uint32_t)r;
     }
@@ -643,7 +709,21 @@ __global__ __launch_bounds__(kThreads, 1) void mgemm_dma_kernel(const uint16_t* 
   auto prefetch = [&](int seq) __attribute__((always_inline)) {
     pf_t = tile_at(seq);
     if (pf_t >= 0) {
-      pf_m = tiles[pf_t / tiles_n];
+      // expert of M-tile mt: the first e whose inclusive tile prefix exceeds mt
+      const int mt = pf_t / tiles_n;
+      int ex = 0;
+      for (int c = 0; c < E; c += 64) {
+        const int ee = c + lane;
+        const uint64_t hit = __ballot(ee < E && s_tp[ee] > mt);
+        if (hit) {
+          ex = c + __ffsll((unsigned long long)hit) - 1;
+          break;
+        }
+      }
+      const int before = ex == 0 ? 0 : s_tp[ex - 1];
+      pf_m.expert = ex;
+      pf_m.row_start = s_rs[ex] + (mt - before) * BM;
+      pf_m.row_end = min(pf_m.row_start + BM, s_re[ex]);
       load_src(pf_m);
     }
   };
@@ -658,15 +738,15 @@ __global__ __launch_bounds__(kThreads, 1) void mgemm_dma_kernel(const uint16_t* 
     rB = make_rsrc(W + (int64_t)ex * w_rows * w_cols, (uint32_t)(w_rows * w_cols * 2));
 #pragma unroll
     for (int i = 0; i < A_INSTR; ++i) {
-      const int row = wave * (BM / 4) + i * 8 + lrow8;
-      const int lc = (lane & 7) ^ kc_swz(row);
+      const int row = wave * A_ROWS + i * RPIK + lrowk;
+      const int lc = lchk ^ kcp_swz<PK>(row);
       a_off[i] = (pf_src[i] * (uint32_t)K + lc * 8) * 2;
     }
     if constexpr (KIND == KIND_NN) {
       iss_n0 = nt * BN;
 #pragma unroll
       for (int i = 0; i < B_INSTR; ++i) {
-        const int kr = wave * 16 + i * NN_RPI + lane / NN_LPR;
+        const int kr = wave * NN_KR + i * NN_RPI + lane / NN_LPR;
         const int lc = (lane % NN_LPR) ^ kr_swz(kr);
         int col = iss_n0 + lc * 8;
         col = col < N ? col : N - 8;
@@ -676,8 +756,8 @@ __global__ __launch_bounds__(kThreads, 1) void mgemm_dma_kernel(const uint16_t* 
       iss_n0 = nt * (BN / 2);
 #pragma unroll
       for (int i = 0; i < B_INSTR; ++i) {
-        const int jr = wave * (BN / 4) + i * 8 + lrow8;
-        const int lc = (lane & 7) ^ kc_swz(jr);
+        const int jr = wave * B_ROWS + i * RPIK + lrowk;
+        const int lc = lchk ^ kcp_swz<PK>(jr);
         int cc = iss_n0 + (jr % (BN / 2));
         cc = cc < N ? cc : N - 1;
         const uint32_t wr = jr < BN / 2 ? (uint32_t)cc : (uint32_t)(N + cc);
@@ -687,8 +767,8 @@ __global__ __launch_bounds__(kThreads, 1) void mgemm_dma_kernel(const uint16_t* 
       iss_n0 = nt * BN;
 #pragma unroll
       for (int i = 0; i < B_INSTR; ++i) {
-        const int jr = wave * (BN / 4) + i * 8 + lrow8;
-        const int lc = (lane & 7) ^ kc_swz(jr);
+        const int jr = wave * B_ROWS + i * RPIK + lrowk;
+        const int lc = lchk ^ kcp_swz<PK>(jr);
         int n = iss_n0 + jr;
         n = n < N ? n : N - 1;
         b_off[i] = ((uint32_t)n * (uint32_t)K + lc * 8) * 2;
@@ -707,16 +787,16 @@ __global__ __launch_bounds__(kThreads, 1) void mgemm_dma_kernel(const uint16_t* 
     }
     char* sa = smem + (issued % STAGES) * STAGE_BYTES;
     char* sb = sa + A_BYTES;
-    const uint32_t ka = (uint32_t)iss_step * (kBK * 2);
+    const uint32_t ka = (uint32_t)iss_step * (BK * 2);
 #pragma unroll
-    for (int i = 0; i < A_INSTR; ++i) dma16(rA, sa + (wave * (BM / 4) + i * 8) * 128, a_off[i], ka);
+    for (int i = 0; i < A_INSTR; ++i) dma16(rA, sa + (wave * A_ROWS + i * RPIK) * PK, a_off[i], ka);
     if constexpr (KIND == KIND_NN) {
-      const uint32_t kb = (uint32_t)iss_step * kBK * (uint32_t)N * 2;
+      const uint32_t kb = (uint32_t)iss_step * BK * (uint32_t)N * 2;
 #pragma unroll
-      for (int i = 0; i < B_INSTR; ++i) dma16(rB, sb + (wave * 16 + i * NN_RPI) * (BN * 2), b_off[i], kb);
+      for (int i = 0; i < B_INSTR; ++i) dma16(rB, sb + (wave * NN_KR + i * NN_RPI) * (BN * 2), b_off[i], kb);
     } else {
 #pragma unroll
-      for (int i = 0; i < B_INSTR; ++i) dma16(rB, sb + (wave * (BN / 4) + i * 8) * 128, b_off[i], ka);
+      for (int i = 0; i < B_INSTR; ++i) dma16(rB, sb + (wave * B_ROWS + i * RPIK) * PK, b_off[i], ka);
     }
     ++iss_step;
     ++issued;
@@ -757,20 +837,20 @@ __global__ __launch_bounds__(kThreads, 1) void mgemm_dma_kernel(const uint16_t* 
         for (int b = 0; b < NB; ++b) {
           int r0;
           if constexpr (KIND == KIND_GATHER_SWIGLU)  // gate blocks, then the matching up blocks
-            r0 = (b < NB / 2 ? 0 : BN / 2) + wn * (BN / 4) + (b % (NB / 2)) * 32;
+            r0 = (b < NB / 2 ? 0 : BN / 2) + wn * (BN / 2 / WGN) + (b % (NB / 2)) * 32;
           else
-            r0 = wn * (BN / 2) + b * 32;
+            r0 = wn * (BN / WGN) + b * 32;
           if constexpr (KIND == KIND_NN) w[b] = tr_operand<BN>(lb, r0, s, lane);
-          else w[b] = lds_read16(lb, kc_off(r0 + (lane & 31), s * 2 + (lane >> 5)));
+          else w[b] = lds_read16(lb, kcp_off<PK>(r0 + (lane & 31), s * 2 + (lane >> 5)));
         }
 #pragma unroll
         for (int a = 0; a < MB; ++a)
-          x[a] = lds_read16(la, kc_off(wm * (BM / 2) + a * 32 + (lane & 31), s * 2 + (lane >> 5)));
+          x[a] = lds_read16(la, kcp_off<PK>(wm * (BM / 2) + a * 32 + (lane & 31), s * 2 + (lane >> 5)));
       };
       load_frags(0, fw[0], fa[0]);
 #pragma unroll
-      for (int s = 0; s < kBK / 16; ++s) {
-        if (s + 1 < kBK / 16) load_frags(s + 1, fw[(s + 1) & 1], fa[(s + 1) & 1]);
+      for (int s = 0; s < BK / 16; ++s) {
+        if (s + 1 < BK / 16) load_frags(s + 1, fw[(s + 1) & 1], fa[(s + 1) & 1]);
 #pragma unroll
         for (int b = 0; b < NB; ++b)
 #pragma unroll
@@ -778,36 +858,64 @@ __global__ __launch_bounds__(kThreads, 1) void mgemm_dma_kernel(const uint16_t* 
       }
     }
 
-    // epilogue: buffer stores over this tile's rows
+    // Epilogue, staged through LDS so that every store writes whole row segments.
+    // The ring slot of the tile's last K step is free once all waves have
+    // passed the barrier below: the next DMA into it is issued only after the
+    // barrier at the top of the next K step.  Each wave stages its own region,
+    // so between its writes and its read-back only in-order LDS execution is
+    // needed.  Staged rows are swizzled at 8-byte granularity (chunk ^ g(row))
+    // so both the 8-byte writes and the 16-byte read-back are conflict-free.
     const int c_rs = __builtin_amdgcn_readfirstlane(comp_rs);
     const int c_rows = __builtin_amdgcn_readfirstlane(comp_re - comp_rs);
     const __amdgpu_buffer_rsrc_t rC = make_rsrc(C + (int64_t)c_rs * N, (uint32_t)c_rows * (uint32_t)N * 2);
+    {
+      constexpr int WCOLS = KIND == KIND_GATHER_SWIGLU ? BN / 2 / WGN : BN / WGN;  // output columns per wave
+      constexpr int PITCH = WCOLS * 2;                                      // staged row bytes
+      constexpr int C8 = PITCH / 8;                                         // 8-byte chunks per row
+      constexpr int RP = 256 / PITCH;                                       // rows per 256 bytes
+      constexpr int REGION = STAGE_BYTES / NW;                              // staging bytes per wave
+      constexpr int FIT = REGION / (32 * PITCH);                            // 32-row blocks that fit
+      constexpr int APP = FIT >= 4 && MB >= 4 ? 4 : (FIT >= 2 && MB >= 2 ? 2 : 1);  // blocks per pass
+      constexpr int LPR = PITCH / 16;                                       // read-back lanes per row
+      constexpr int RPI = 64 / LPR;                                         // rows per read-back
+      static_assert(FIT >= 1 && MB % APP == 0 && RP * C8 == 32, "staging layout");
+      char* stg = smem + ((g0 + nk - 1) % STAGES) * STAGE_BYTES + wave * REGION;
+      const int col0 = comp_n0 + wn * WCOLS;
+      barrier_lds();
 #pragma unroll
-    for (int a = 0; a < MB; ++a) {
-      const uint32_t ml = (uint32_t)(wm * (BM / 2) + a * 32 + (lane & 31));  // row within the tile
-      if constexpr (KIND == KIND_GATHER_SWIGLU) {
+      for (int a0 = 0; a0 < MB; a0 += APP) {
 #pragma unroll
-        for (int b = 0; b < NB / 2; ++b)
+        for (int a = a0; a < a0 + APP; ++a) {
+          const int r = (a - a0) * 32 + (lane & 31);
+          const int g = (r / RP) % C8;
 #pragma unroll
-          for (int gq = 0; gq < 4; ++gq) {
-            const int c = comp_n0 + wn * (BN / 4) + b * 32 + gq * 8 + (lane >> 5) * 4;
-            float o[4];
+          for (int b = 0; b < WCOLS / 32; ++b)
 #pragma unroll
-            for (int q = 0; q < 4; ++q)
-              o[q] = swiglu_fast<TR>(acc[b][a][gq * 4 + q], acc[b + NB / 2][a][gq * 4 + q]);
-            const uint32_t voff = c < N ? (ml * (uint32_t)N + (uint32_t)c) * 2 : 0x80000000u;
-            bstore8(rC, voff, pack4<TR>(o[0], o[1], o[2], o[3]));
-          }
-      } else {
+            for (int gq = 0; gq < 4; ++gq) {
+              float o[4];
 #pragma unroll
-        for (int b = 0; b < NB; ++b)
+              for (int q = 0; q < 4; ++q) {
+                if constexpr (KIND == KIND_GATHER_SWIGLU)
+                  o[q] = swiglu_fast<TR>(acc[b][a][gq * 4 + q], acc[b + NB / 2][a][gq * 4 + q]);
+                else
+                  o[q] = acc[b][a][gq * 4 + q];
+              }
+              const int ch8 = (b * 32 + gq * 8) / 4 + (lane >> 5);
+              *reinterpret_cast<u32x2*>(stg + r * PITCH + ((ch8 ^ g) << 3)) = pack4<TR>(o[0], o[1], o[2], o[3]);
+            }
+        }
 #pragma unroll
-          for (int gq = 0; gq < 4; ++gq) {
-            const int c = comp_n0 + wn * (BN / 2) + b * 32 + gq * 8 + (lane >> 5) * 4;
-            const uint32_t voff = c < N ? (ml * (uint32_t)N + (uint32_t)c) * 2 : 0x80000000u;
-            bstore8(rC, voff, pack4<TR>(acc[b][a][gq * 4 + 0], acc[b][a][gq * 4 + 1], acc[b][a][gq * 4 + 2],
-                                        acc[b][a][gq * 4 + 3]));
-          }
+        for (int i = 0; i < APP * 32 / RPI; ++i) {
+          const int r = i * RPI + lane / LPR;
+          const int c16 = lane % LPR;
+          const int g = (r / RP) % C8;
+          u32x4 v = *reinterpret_cast<const u32x4*>(stg + r * PITCH + ((c16 ^ (g >> 1)) << 4));
+          if (g & 1) v = u32x4{v[2], v[3], v[0], v[1]};
+          const uint32_t ml = (uint32_t)(wm * (BM / 2) + a0 * 32 + r);
+          const int c = col0 + c16 * 8;
+          const uint32_t voff = c < N ? (ml * (uint32_t)N + (uint32_t)c) * 2 : 0x80000000u;
+          bstore16(rC, voff, v);
+        }
       }
     }
 
@@ -950,13 +1058,13 @@ int cu_margin() {
 
 // Persistent grid: (CUs - margin) x resident workgroups per CU, rounded down to a multiple of 8.
 template <typename KernelT>
-int persistent_grid(KernelT kernel) {
+int persistent_grid(KernelT kernel, int threads = kThreads, size_t dyn_lds = 0) {
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess) return 8;
   int cus = 0;
   if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus < 1) cus = 8;
   int occ = 1;
-  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, kernel, kThreads, 0) != hipSuccess || occ < 1) occ = 1;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, kernel, threads, dyn_lds) != hipSuccess || occ < 1) occ = 1;
   int g = (cus - cu_margin()) * occ;
   g = (g / 8) * 8;
   return g < 8 ? 8 : g;
@@ -986,41 +1094,51 @@ int launch_mgemm(const void* A, const int32_t* gather, const void* W, const int6
   return HRM_MOE_OK;
 }
 
-template <typename TR, int KIND, int BM, int BN, int STAGES>
+template <typename TR, int KIND, int BM, int BN, int STAGES, int NW, int BK>
 int launch_mgemm_dma(const void* A, const int32_t* gather, const void* W, const int64_t* tpe, int64_t M, int N,
                      int K, int E, int64_t a_rows, void* C, void* workspace, void* stream) {
-  GemmWs w = carve(workspace, M, E, kBMMin);
-  const int max_tiles = (int)((M + BM - 1) / BM + E);
-  HRM_LAUNCH(plan_kernel, dim3(1), dim3(1024), 0, stream, tpe, E, M, BM, w.tiles, max_tiles, w.count, w.row_offsets,
-             w.work_counter);
+  (void)workspace;  // the DMA kernels plan their tiles themselves
   const int tiles_n = KIND == KIND_GATHER_SWIGLU ? (N + BN / 2 - 1) / (BN / 2) : (N + BN - 1) / BN;
-  auto kern = mgemm_dma_kernel<TR, KIND, BM, BN, STAGES>;
-  static int grid = 0;
-  if (grid == 0) grid = persistent_grid(kern);
-  HRM_LAUNCH(kern, dim3(grid), dim3(kThreads), 0, stream, (const uint16_t*)A, gather, (const uint16_t*)W,
-             (uint16_t*)C, w.tiles, w.count, N, K, tiles_n, (uint32_t)(a_rows * K * 2));
+  auto kern = mgemm_dma_kernel<TR, KIND, BM, BN, STAGES, NW, BK>;
+  const size_t plan_bytes = sizeof(int) * 3 * (size_t)E;
+  static int grid = 0, grid_e = -1;
+  if (grid == 0 || grid_e != E) {
+    grid = persistent_grid(kern, NW * 64, plan_bytes);
+    grid_e = E;
+  }
+  HRM_LAUNCH(kern, dim3(grid), dim3(NW * 64), plan_bytes, stream, (const uint16_t*)A, gather, (const uint16_t*)W,
+             (uint16_t*)C, tpe, E, (int)M, N, K, tiles_n, (uint32_t)(a_rows * K * 2));
   return HRM_MOE_OK;
 }
 
-// Tile shape and pipeline depth of the DMA kernels.  Default: 128 x 128 tiles
-// with 2 stages (64 KB of LDS, two workgroups per CU).
-// HRM_MOE_GEMM_CFG="<rows>x<cols>x<stages>" (e.g. "256x128x3") overrides it.
+// Tile shape, pipeline depth, waves and K step of the DMA kernels.
+// Default: 256 x 256 tiles with 8 waves (2 per SIMD, 128 x 64 per wave) and 2
+// stages of 64-wide K steps (128 KB of LDS) when experts average at least 256
+// rows and the weight rows split into whole 256-row tiles; otherwise 128 x 128
+// tiles, 4 waves, 2 stages (64 KB of LDS, two workgroups per CU).  The large
+// tile halves LDS and L2 traffic per flop; the small one wastes less on ragged
+// experts and on widths that are not multiples of 256.
+// HRM_MOE_GEMM_CFG="<rows>x<cols>x<stages>x<waves>x<kstep>" (e.g.
+// "256x256x5x8x32") overrides the choice with one of the built variants.
 struct MCfg {
-  int bm, bn, stages;
+  int bm, bn, stages, waves, bk;
 };
-MCfg mgemm_cfg(int64_t M, int E) {
+bool mcfg_built(const MCfg& c) {
+  if (c.bm == 128 && c.bn == 128 && c.waves == 4)
+    return (c.bk == 64 && (c.stages == 2 || c.stages == 3)) || (c.bk == 32 && (c.stages == 4 || c.stages == 5));
+  if (c.bm == 256 && c.bn == 256 && c.waves == 8)
+    return (c.bk == 64 && c.stages == 2) || (c.bk == 32 && (c.stages == 4 || c.stages == 5));
+  return false;
+}
+MCfg mgemm_cfg(int64_t M, int E, int64_t w_rows) {
   static const char* env = getenv("HRM_MOE_GEMM_CFG");
   if (env) {
-    int bm = 0, bn = 0, st = 0;
-    if (sscanf(env, "%dx%dx%d", &bm, &bn, &st) == 3) {
-      if ((bm == 256 && bn == 256 && st == 2) || (bm == 256 && bn == 128 && st >= 2 && st <= 3) ||
-          (bm == 128 && bn == 128 && st >= 2 && st <= 4))
-        return {bm, bn, st};
-    }
+    MCfg c{0, 0, 0, 4, 64};
+    const int n = sscanf(env, "%dx%dx%dx%dx%d", &c.bm, &c.bn, &c.stages, &c.waves, &c.bk);
+    if (n >= 3 && mcfg_built(c)) return c;
   }
-  (void)M;
-  (void)E;
-  return MCfg{128, 128, 2};
+  if (M >= (int64_t)E * 256 && w_rows % 256 == 0) return MCfg{256, 256, 2, 8, 64};
+  return MCfg{128, 128, 2, 4, 64};
 }
 
 template <typename TR, int KIND>
@@ -1034,19 +1152,29 @@ int dispatch_mgemm_t(const void* A, const int32_t* gather, const void* W, const 
     return M >= (int64_t)E * 192 ? launch_mgemm<TR, KIND, 256, 128>(A, gather, W, tpe, M, N, K, E, C, workspace, stream)
                                  : launch_mgemm<TR, KIND, 128, 128>(A, gather, W, tpe, M, N, K, E, C, workspace, stream);
   }
-  MCfg c = mgemm_cfg(M, E);
-  // the ring may run at most one tile ahead: STAGES - 1 <= K / 64
-  if (c.stages - 1 > K / kBK) c.stages = K / kBK + 1;
-#define HRM_MG(BM_, BN_, ST_) \
-  return launch_mgemm_dma<TR, KIND, BM_, BN_, ST_>(A, gather, W, tpe, M, N, K, E, a_rows, C, workspace, stream)
-  if (c.bm == 256 && c.bn == 256) HRM_MG(256, 256, 2);
-  if (c.bm == 256) {
-    if (c.stages == 2) HRM_MG(256, 128, 2);
-    HRM_MG(256, 128, 3);
+  // weight rows spanned by the N tiles: 2N for the gate/up pair, else N
+  MCfg c = mgemm_cfg(M, E, KIND == KIND_GATHER_SWIGLU ? 2 * (int64_t)N : (int64_t)N);
+  if (K % c.bk != 0) c = MCfg{128, 128, 2, 4, 64};
+  // the ring may run at most one tile ahead: STAGES - 1 <= K / BK
+  if (c.stages - 1 > K / c.bk) {
+    if (c.bk == 32) c = MCfg{c.bm, c.bn, 2, c.waves, 64};
+    else c.stages = 2;
   }
-  if (c.stages == 2) HRM_MG(128, 128, 2);
-  if (c.stages == 3) HRM_MG(128, 128, 3);
-  HRM_MG(128, 128, 4);
+#define HRM_MG(BM_, BN_, ST_, NW_, BK_) \
+  return launch_mgemm_dma<TR, KIND, BM_, BN_, ST_, NW_, BK_>(A, gather, W, tpe, M, N, K, E, a_rows, C, workspace, stream)
+  if (c.bm == 256) {
+    if (c.bk == 32) {
+      if (c.stages == 5) HRM_MG(256, 256, 5, 8, 32);
+      HRM_MG(256, 256, 4, 8, 32);
+    }
+    HRM_MG(256, 256, 2, 8, 64);
+  }
+  if (c.bk == 32) {
+    if (c.stages == 5) HRM_MG(128, 128, 5, 4, 32);
+    HRM_MG(128, 128, 4, 4, 32);
+  }
+  if (c.stages == 3) HRM_MG(128, 128, 3, 4, 64);
+  HRM_MG(128, 128, 2, 4, 64);
 #undef HRM_MG
 }
 

@@ -99,11 +99,23 @@ __global__ __launch_bounds__(kPermThreads) void permute_rank_kernel(const int64_
   }
 }
 
-// One workgroup of 1024 threads.  With E + 1 <= 1024 buckets, bucket b's nb
-// block counts are split over G = 1024 / (E+1) threads: each sums a contiguous
-// range of blocks, the G partial sums are scanned in LDS, then each thread
-// writes the bases of its range.  With more buckets (E = 1024) each thread
-// walks whole buckets.
+// Inclusive scan across the 64 lanes of a wave.
+__device__ __forceinline__ int32_t wave_incl_scan(int32_t v, int lane) {
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const int32_t u = __shfl_up(v, o, 64);
+    if (lane >= o) v += u;
+  }
+  return v;
+}
+
+// One workgroup of 1024 threads.  The per-block counts form a [nb][E+1]
+// matrix.  With E + 1 <= 512 buckets, G = 1024 / (E+1) groups of E+1
+// consecutive threads each own a contiguous range of blocks, so a group reads
+// and writes whole matrix rows (coalesced).  Each thread sums its bucket over
+// its range; one thread per bucket scans the G partials; wave 0 scans the
+// bucket totals; each thread then writes the bases of its range.  With more
+// buckets each thread walks whole buckets.
 __global__ __launch_bounds__(1024) void permute_scan_kernel(const int32_t* __restrict__ counts, int nb, int E,
                                                             int32_t* __restrict__ base,
                                                             int64_t* __restrict__ tokens_per_expert,
@@ -113,11 +125,12 @@ __global__ __launch_bounds__(1024) void permute_scan_kernel(const int32_t* __res
   __shared__ int32_t off[kMaxExperts + 2];
   const int nbk = E + 1;
   const int tid = threadIdx.x;
-  const bool split = nbk <= 1024;
+  const int lane = tid & 63;
+  const bool split = nbk <= 512;
   const int G = split ? 1024 / nbk : 1;
   const int per = (nb + G - 1) / G;
-  const int b = tid / G, g = tid % G;
-  const bool on = split && b < nbk;
+  const int b = tid % nbk, g = tid / nbk;
+  const bool on = split && g < G;
   const int j0 = g * per, j1 = min(nb, j0 + per);
   if (split) {
     int32_t sum = 0;
@@ -128,8 +141,8 @@ __global__ __launch_bounds__(1024) void permute_scan_kernel(const int32_t* __res
     if (on && g == 0) {
       int32_t run = 0;
       for (int u = 0; u < G; ++u) {
-        const int32_t v = part[tid + u];
-        part[tid + u] = run;
+        const int32_t v = part[u * nbk + b];
+        part[u * nbk + b] = run;
         run += v;
       }
       tot[b] = run;
@@ -142,11 +155,14 @@ __global__ __launch_bounds__(1024) void permute_scan_kernel(const int32_t* __res
     }
   }
   __syncthreads();
-  if (tid == 0) {
-    int32_t run = 0;
-    for (int bb = 0; bb < nbk; ++bb) {
-      off[bb] = run;
-      run += tot[bb];
+  if (tid < 64) {  // exclusive scan of the bucket totals, 64 at a time
+    int32_t carry = 0;
+    for (int c = 0; c < nbk; c += 64) {
+      const int bb = c + lane;
+      const int32_t v = bb < nbk ? tot[bb] : 0;
+      const int32_t incl = wave_incl_scan(v, lane);
+      if (bb < nbk) off[bb] = carry + incl - v;
+      carry += __shfl(incl, 63, 64);
     }
   }
   __syncthreads();
