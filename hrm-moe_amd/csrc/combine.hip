@@ -58,7 +58,10 @@ struct Elem<HRM_MOE_F32> {
 constexpr int kWavesPerBlock = 4;
 constexpr int kMaxTopK = 32;
 
-template <int DT>
+// KU > 0: top-k fixed at compile time, so every row load of a chunk is issued
+// before the first product is added (all k loads in flight per lane).
+// KU == 0: any top-k up to kMaxTopK, rows loaded one after another.
+template <int DT, int KU>
 __global__ __launch_bounds__(kWavesPerBlock * 64) void combine_kernel(const char* __restrict__ Y,
                                                                      const int32_t* __restrict__ slot_to_row,
                                                                      const void* __restrict__ wts,
@@ -93,20 +96,63 @@ __global__ __launch_bounds__(kWavesPerBlock * 64) void combine_kernel(const char
   __syncthreads();
   if (!active) return;
   const int64_t chunks = H / P;
-  for (int64_t c = lane; c < chunks; c += 64) {
-    float acc[P];
+  if constexpr (KU > 0) {
+    int64_t roff[KU];
+    float wj[KU];
+    bool ok[KU];
 #pragma unroll
-    for (int q = 0; q < P; ++q) acc[q] = 0.0f;
-    for (int j = 0; j < k; ++j) {
+    for (int j = 0; j < KU; ++j) {
       const int32_t r = s_row[wv][j];
-      if (r >= r_valid) continue;
-      const float wj = s_w[wv][j];
-      const u32x4 y = ld16(Y + ((int64_t)r * H + c * P) * ESZ);
-#pragma unroll
-      for (int q = 0; q < P; ++q) acc[q] += El::round(El::get(y, q) * wj);
+      ok[j] = r < r_valid;  // dropped rows hold no expert output
+      roff[j] = (int64_t)(ok[j] ? r : 0) * H;
+      wj[j] = s_w[wv][j];
     }
-    st16(out + (t * H + c * P) * ESZ, El::pack(acc));
+    for (int64_t c = lane; c < chunks; c += 64) {
+      u32x4 y[KU];
+#pragma unroll
+      for (int j = 0; j < KU; ++j) y[j] = ld16(Y + (roff[j] + c * P) * ESZ);
+      float acc[P];
+#pragma unroll
+      for (int q = 0; q < P; ++q) acc[q] = 0.0f;
+#pragma unroll
+      for (int j = 0; j < KU; ++j)
+#pragma unroll
+        for (int q = 0; q < P; ++q) acc[q] = ok[j] ? acc[q] + El::round(El::get(y[j], q) * wj[j]) : acc[q];
+      st16(out + (t * H + c * P) * ESZ, El::pack(acc));
+    }
+  } else {
+    for (int64_t c = lane; c < chunks; c += 64) {
+      float acc[P];
+#pragma unroll
+      for (int q = 0; q < P; ++q) acc[q] = 0.0f;
+      for (int j = 0; j < k; ++j) {
+        const int32_t r = s_row[wv][j];
+        if (r >= r_valid) continue;
+        const float wj = s_w[wv][j];
+        const u32x4 y = ld16(Y + ((int64_t)r * H + c * P) * ESZ);
+#pragma unroll
+        for (int q = 0; q < P; ++q) acc[q] += El::round(El::get(y, q) * wj);
+      }
+      st16(out + (t * H + c * P) * ESZ, El::pack(acc));
+    }
   }
+}
+
+template <int DT>
+void launch_combine(dim3 grid, dim3 block, void* stream, const char* Y, const int32_t* slot_to_row, const void* wts,
+                    const int32_t* offs, int64_t T, int k, int64_t H, int E, char* O) {
+  if (k == 8)
+    hipLaunchKernelGGL((combine_kernel<DT, 8>), grid, block, 0, (hipStream_t)stream, Y, slot_to_row, wts, offs, T, k, H,
+                       E, O);
+  else if (k == 2)
+    hipLaunchKernelGGL((combine_kernel<DT, 2>), grid, block, 0, (hipStream_t)stream, Y, slot_to_row, wts, offs, T, k, H,
+                       E, O);
+  else if (k == 4)
+    hipLaunchKernelGGL((combine_kernel<DT, 4>), grid, block, 0, (hipStream_t)stream, Y, slot_to_row, wts, offs, T, k, H,
+                       E, O);
+  else
+    hipLaunchKernelGGL((combine_kernel<DT, 0>), grid, block, 0, (hipStream_t)stream, Y, slot_to_row, wts, offs, T, k, H,
+                       E, O);
 }
 
 }  // namespace
@@ -124,13 +170,15 @@ extern "C" int hrm_moe_combine(const void* expert_out, const int32_t* slot_to_ro
   const char* Y = static_cast<const char*>(expert_out);
   char* O = static_cast<char*>(out);
   if (dtype == HRM_MOE_BF16)
-    HRM_LAUNCH(hrm::combine_kernel<HRM_MOE_BF16>, grid, block, 0, stream, Y, slot_to_row, topk_weight, expert_offsets,
-               num_tokens, top_k, hidden_size, num_experts, O);
+    hrm::launch_combine<HRM_MOE_BF16>(grid, block, stream, Y, slot_to_row, topk_weight, expert_offsets, num_tokens,
+                                      top_k, hidden_size, num_experts, O);
   else if (dtype == HRM_MOE_F16)
-    HRM_LAUNCH(hrm::combine_kernel<HRM_MOE_F16>, grid, block, 0, stream, Y, slot_to_row, topk_weight, expert_offsets,
-               num_tokens, top_k, hidden_size, num_experts, O);
+    hrm::launch_combine<HRM_MOE_F16>(grid, block, stream, Y, slot_to_row, topk_weight, expert_offsets, num_tokens,
+                                     top_k, hidden_size, num_experts, O);
   else
-    HRM_LAUNCH(hrm::combine_kernel<HRM_MOE_F32>, grid, block, 0, stream, Y, slot_to_row, topk_weight, expert_offsets,
-               num_tokens, top_k, hidden_size, num_experts, O);
+    hrm::launch_combine<HRM_MOE_F32>(grid, block, stream, Y, slot_to_row, topk_weight, expert_offsets, num_tokens,
+                                     top_k, hidden_size, num_experts, O);
+  const hipError_t err = hipGetLastError();
+  if (err != hipSuccess) return (int)err;
   return HRM_MOE_OK;
 }

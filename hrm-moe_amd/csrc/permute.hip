@@ -134,8 +134,10 @@ __global__ __launch_bounds__(1024) void permute_scan_kernel(const int32_t* __res
   const int j0 = g * per, j1 = min(nb, j0 + per);
   if (split) {
     int32_t sum = 0;
-    if (on)
+    if (on) {
+#pragma unroll 8
       for (int j = j0; j < j1; ++j) sum += counts[(int64_t)j * nbk + b];
+    }
     part[tid] = sum;
     __syncthreads();
     if (on && g == 0) {
@@ -169,6 +171,7 @@ __global__ __launch_bounds__(1024) void permute_scan_kernel(const int32_t* __res
   if (split) {
     if (on) {
       int32_t run = off[b] + part[tid];
+#pragma unroll 8
       for (int j = j0; j < j1; ++j) {
         const int32_t c = counts[(int64_t)j * nbk + b];
         base[(int64_t)j * nbk + b] = run;

@@ -4,16 +4,24 @@
 //   probs = F.softmax(logits, -1, dtype=float32)
 //   w, idx = torch.topk(probs, k);  w = w / w.sum(-1).clamp_min(1e-12);  w.to(dtype)
 //
-// Layout: four lanes own one token row; lane q holds the contiguous experts
-// [q*C, (q+1)*C) with C = NP2/4 (NP2 = padded expert count).  Cross-lane
-// steps use quad DPP moves, so a wave handles 16 rows.
+// Layout: LPR lanes (a quad, or a DPP row of 16) own one token row; lane q
+// holds the contiguous experts [q*C, (q+1)*C) with C = NP2/LPR (NP2 = padded
+// expert count).  Cross-lane steps are DPP moves inside the row: quad
+// permutations for lane distances 1 and 2, row rotations for 4 and 8.  The
+// launcher uses quads: the ordering network and weight sum run once per row
+// group of a wave, so 16 rows per wave issue fewer instructions in total than
+// 4 rows per wave, even though each selection round is longer.
 //
 // Bit-exactness with torch on the device:
 //  * softmax: torch's persistent softmax reduces a row across a wavefront with
 //    an xor butterfly.  For padded size NP2 that is the pairwise tree
-//    S_i <- S_i + S_{i+o}, o = NP2/2 ... 1.  Levels o >= C pair lanes (xor 2,
-//    xor 1); levels o < C stay inside a lane.  exp is expf, and the division is
-//    IEEE.  Padding experts hold exp(-inf) = 0, which leaves every partial sum unchanged.
+//    S_i <- S_i + S_{i+o}, o = NP2/2 ... 1.  Levels o >= C pair lanes q and
+//    q ^ (o/C); levels o < C stay inside a lane.  Levels run from the largest
+//    distance down, so when a rotation by 4 replaces xor 4 the lanes it
+//    reads hold the same sums as their xor partners (rotation by 8 is xor 8
+//    in a row of 16).  Additions are commutative, so every lane of the row ends
+//    with the same bits.  exp is expf, and the division is IEEE.  Padding
+//    experts hold exp(-inf) = 0, which leaves every partial sum unchanged.
 //  * top-k: selection in (value desc, index asc) order, then torch's output
 //    order and weight-sum order from topk_order.h.
 #include "common.h"
@@ -22,14 +30,17 @@
 namespace hrm {
 namespace {
 
-__device__ __forceinline__ float dpp_xor1(float x) {
-  return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), 0xB1, 0xF, 0xF, false));  // quad_perm [1,0,3,2]
+// Value of the lane at distance D inside the row (D = 1, 2: xor; D = 4, 8:
+// rotation within a row of 16 lanes).
+template <int D>
+__device__ __forceinline__ uint32_t xlane(uint32_t x) {
+  constexpr int ctrl = D == 1 ? 0xB1 : D == 2 ? 0x4E : D == 4 ? 0x124 : 0x128;  // quad_perm / row_ror
+  return (uint32_t)__builtin_amdgcn_mov_dpp((int)x, ctrl, 0xF, 0xF, false);
 }
-__device__ __forceinline__ float dpp_xor2(float x) {
-  return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), 0x4E, 0xF, 0xF, false));  // quad_perm [2,3,0,1]
+template <int D>
+__device__ __forceinline__ float xlanef(float x) {
+  return __uint_as_float(xlane<D>(__float_as_uint(x)));
 }
-__device__ __forceinline__ uint32_t dpp_xor1u(uint32_t x) { return (uint32_t)__builtin_amdgcn_mov_dpp((int)x, 0xB1, 0xF, 0xF, false); }
-__device__ __forceinline__ uint32_t dpp_xor2u(uint32_t x) { return (uint32_t)__builtin_amdgcn_mov_dpp((int)x, 0x4E, 0xF, 0xF, false); }
 
 __device__ __forceinline__ float load_logit(const void* p, int dt, int64_t i) {
   if (dt == HRM_MOE_BF16) return BF16::to_f(reinterpret_cast<const uint16_t*>(p)[i]);
@@ -43,9 +54,9 @@ __device__ __forceinline__ void store_weight(void* p, int dt, int64_t i, float w
   else reinterpret_cast<float*>(p)[i] = w;
 }
 
-// One selection round over a quad: the largest remaining key, ties to the lower
-// expert index; the winner's key is cleared in the lane that holds it.
-template <int C>
+// One selection round over the row's lanes: the largest remaining key, ties
+// to the lower expert index; the winner's key is cleared in the lane that holds it.
+template <int C, int LPR>
 __device__ __forceinline__ void select_round(uint32_t (&key)[C], int e0, uint32_t& out_key, int& out_idx) {
   uint32_t bk = 0u;
   int be = 0x7fffffff;
@@ -53,12 +64,15 @@ __device__ __forceinline__ void select_round(uint32_t (&key)[C], int e0, uint32_
   for (int j = 0; j < C; ++j) {
     if (key[j] > bk) { bk = key[j]; be = e0 + j; }
   }
-  uint32_t ok = dpp_xor1u(bk);
-  int oe = (int)dpp_xor1u((uint32_t)be);
-  if (ok > bk || (ok == bk && oe < be)) { bk = ok; be = oe; }
-  ok = dpp_xor2u(bk);
-  oe = (int)dpp_xor2u((uint32_t)be);
-  if (ok > bk || (ok == bk && oe < be)) { bk = ok; be = oe; }
+  auto merge = [&](uint32_t ok, int oe) __attribute__((always_inline)) {
+    if (ok > bk || (ok == bk && oe < be)) { bk = ok; be = oe; }
+  };
+  if constexpr (LPR == 16) {
+    merge(xlane<8>(bk), (int)xlane<8>((uint32_t)be));
+    merge(xlane<4>(bk), (int)xlane<4>((uint32_t)be));
+  }
+  merge(xlane<2>(bk), (int)xlane<2>((uint32_t)be));
+  merge(xlane<1>(bk), (int)xlane<1>((uint32_t)be));
 #pragma unroll
   for (int j = 0; j < C; ++j) {
     if (e0 + j == be) key[j] = 0u;
@@ -67,15 +81,19 @@ __device__ __forceinline__ void select_round(uint32_t (&key)[C], int e0, uint32_
   out_idx = be;
 }
 
-template <int NP2, int SLOTS>
+template <int NP2, int SLOTS, int LPR>
 __global__ __launch_bounds__(256) void router_topk_kernel(const void* __restrict__ logits, int ldt, int64_t T, int E,
                                                           int k, int norm, float* __restrict__ probs,
                                                           int64_t* __restrict__ idx_out, void* __restrict__ w_out,
                                                           int wdt) {
-  constexpr int C = NP2 / 4;
-  const int q = threadIdx.x & 3;
-  const int64_t row = (int64_t)blockIdx.x * 64 + (threadIdx.x >> 2);
-  const bool active = row < T;  // inactive lanes still take part in the quad exchanges
+  constexpr int C = NP2 / LPR;
+  constexpr int RPB = 256 / LPR;  // rows per block
+  static_assert(LPR == 4 || LPR == 16, "4 or 16 lanes per row");
+  static_assert(C >= 1 && (C & (C - 1)) == 0, "experts per lane");
+  const int q = threadIdx.x % LPR;
+  const int lr = threadIdx.x / LPR;
+  const int64_t row = (int64_t)blockIdx.x * RPB + lr;
+  const bool active = row < T;  // inactive lanes still take part in the row exchanges
   const int e0 = q * C;
 
   float s[C];
@@ -88,8 +106,12 @@ __global__ __launch_bounds__(256) void router_topk_kernel(const void* __restrict
     s[j] = x;
     mx = fmaxf(mx, x);
   }
-  mx = fmaxf(mx, dpp_xor1(mx));
-  mx = fmaxf(mx, dpp_xor2(mx));
+  if constexpr (LPR == 16) {
+    mx = fmaxf(mx, xlanef<8>(mx));
+    mx = fmaxf(mx, xlanef<4>(mx));
+  }
+  mx = fmaxf(mx, xlanef<2>(mx));
+  mx = fmaxf(mx, xlanef<1>(mx));
 
   float t[C];
 #pragma unroll
@@ -98,10 +120,16 @@ __global__ __launch_bounds__(256) void router_topk_kernel(const void* __restrict
     t[j] = s[j];
   }
   // Pairwise tree of the wavefront butterfly: cross-lane levels first.
+  if constexpr (LPR == 16) {
 #pragma unroll
-  for (int j = 0; j < C; ++j) t[j] = t[j] + dpp_xor2(t[j]);
+    for (int j = 0; j < C; ++j) t[j] = t[j] + xlanef<8>(t[j]);
 #pragma unroll
-  for (int j = 0; j < C; ++j) t[j] = t[j] + dpp_xor1(t[j]);
+    for (int j = 0; j < C; ++j) t[j] = t[j] + xlanef<4>(t[j]);
+  }
+#pragma unroll
+  for (int j = 0; j < C; ++j) t[j] = t[j] + xlanef<2>(t[j]);
+#pragma unroll
+  for (int j = 0; j < C; ++j) t[j] = t[j] + xlanef<1>(t[j]);
 #pragma unroll
   for (int o = C / 2; o > 0; o /= 2) {
 #pragma unroll
@@ -119,7 +147,7 @@ __global__ __launch_bounds__(256) void router_topk_kernel(const void* __restrict
     key[j] = ok ? (__float_as_uint(p) + 1u) : 0u;  // 0 marks "not selectable"
   }
 
-  // Top-k selection in (value desc, index asc) order: k rounds of a quad-wide
+  // Top-k selection in (value desc, index asc) order: k rounds of a row-wide
   // argmax (ties to the lower expert index), each removing its winner.
   if constexpr (SLOTS <= 8) {
     uint32_t sk[SLOTS];
@@ -128,7 +156,7 @@ __global__ __launch_bounds__(256) void router_topk_kernel(const void* __restrict
     for (int r = 0; r < SLOTS; ++r) {
       sk[r] = 0u;
       si[r] = 0;
-      if (r < k) select_round<C>(key, e0, sk[r], si[r]);
+      if (r < k) select_round<C, LPR>(key, e0, sk[r], si[r]);
     }
     if (!active) return;
     uint32_t gk[SLOTS];
@@ -145,23 +173,22 @@ __global__ __launch_bounds__(256) void router_topk_kernel(const void* __restrict
     }
 #pragma unroll
     for (int j = 0; j < SLOTS; ++j) {
-      if (j < k && (j & 3) == q) {
+      if (j < k && (j % LPR) == q) {
         idx_out[row * k + j] = (int64_t)gi[j];
         store_weight(w_out, wdt, row * k + j, w[j]);
       }
     }
   } else {
     // k > 8: the ordering runs in loop form on this row's LDS arrays (one lane per row).
-    __shared__ uint32_t s_sk[64][SLOTS];
-    __shared__ int s_si[64][SLOTS];
-    __shared__ uint32_t s_gk[64][SLOTS];
-    __shared__ int s_gi[64][SLOTS];
-    __shared__ bool s_gv[64][SLOTS];
-    const int lr = threadIdx.x >> 2;
+    __shared__ uint32_t s_sk[RPB][SLOTS];
+    __shared__ int s_si[RPB][SLOTS];
+    __shared__ uint32_t s_gk[RPB][SLOTS];
+    __shared__ int s_gi[RPB][SLOTS];
+    __shared__ bool s_gv[RPB][SLOTS];
     for (int r = 0; r < k; ++r) {
       uint32_t bk;
       int be;
-      select_round<C>(key, e0, bk, be);
+      select_round<C, LPR>(key, e0, bk, be);
       if (q == 0) {
         s_sk[lr][r] = bk;
         s_si[lr][r] = be;
@@ -183,23 +210,27 @@ __global__ __launch_bounds__(256) void router_topk_kernel(const void* __restrict
   }
 }
 
-template <int NP2>
+template <int NP2, int LPR>
 int launch_router_np2(const void* logits, int ldt, int64_t T, int E, int k, int norm, float* probs, int64_t* idx,
                       void* w, int wdt, void* stream) {
-  dim3 grid((unsigned)((T + 63) / 64)), block(256);
-  if (k <= 2) HRM_LAUNCH((router_topk_kernel<NP2, 2>), grid, block, 0, stream, logits, ldt, T, E, k, norm, probs, idx, w, wdt);
-  else if (k <= 4) HRM_LAUNCH((router_topk_kernel<NP2, 4>), grid, block, 0, stream, logits, ldt, T, E, k, norm, probs, idx, w, wdt);
-  else if (k <= 8) HRM_LAUNCH((router_topk_kernel<NP2, 8>), grid, block, 0, stream, logits, ldt, T, E, k, norm, probs, idx, w, wdt);
+  constexpr int RPB = 256 / LPR;
+  dim3 grid((unsigned)((T + RPB - 1) / RPB)), block(256);
+#define HRM_RT(SL) \
+  HRM_LAUNCH((router_topk_kernel<NP2, SL, LPR>), grid, block, 0, stream, logits, ldt, T, E, k, norm, probs, idx, w, wdt)
+  if (k <= 2) HRM_RT(2);
+  else if (k <= 4) HRM_RT(4);
+  else if (k <= 8) HRM_RT(8);
   else if constexpr (NP2 >= 16) {
-    if (k <= 16) HRM_LAUNCH((router_topk_kernel<NP2, 16>), grid, block, 0, stream, logits, ldt, T, E, k, norm, probs, idx, w, wdt);
+    if (k <= 16) HRM_RT(16);
     else if constexpr (NP2 >= 32) {
-      HRM_LAUNCH((router_topk_kernel<NP2, 32>), grid, block, 0, stream, logits, ldt, T, E, k, norm, probs, idx, w, wdt);
+      HRM_RT(32);
     } else {
       return HRM_MOE_ERR_UNSUPPORTED;
     }
   } else {
     return HRM_MOE_ERR_UNSUPPORTED;
   }
+#undef HRM_RT
   return HRM_MOE_OK;
 }
 
@@ -216,7 +247,7 @@ extern "C" int hrm_moe_router_topk(const void* logits, int logits_dtype, int64_t
   if (num_tokens == 0) return HRM_MOE_OK;
   if (!logits || !topk_idx || !topk_weight) return HRM_MOE_ERR_INVALID;
   const int E = num_experts, k = top_k;
-  if (E <= 8) return hrm::launch_router_np2<8>(logits, logits_dtype, num_tokens, E, k, norm_topk_prob, probs, topk_idx, topk_weight, weight_dtype, stream);
-  if (E <= 64) return hrm::launch_router_np2<64>(logits, logits_dtype, num_tokens, E, k, norm_topk_prob, probs, topk_idx, topk_weight, weight_dtype, stream);
-  return hrm::launch_router_np2<128>(logits, logits_dtype, num_tokens, E, k, norm_topk_prob, probs, topk_idx, topk_weight, weight_dtype, stream);
+  if (E <= 8) return hrm::launch_router_np2<8, 4>(logits, logits_dtype, num_tokens, E, k, norm_topk_prob, probs, topk_idx, topk_weight, weight_dtype, stream);
+  if (E <= 64) return hrm::launch_router_np2<64, 4>(logits, logits_dtype, num_tokens, E, k, norm_topk_prob, probs, topk_idx, topk_weight, weight_dtype, stream);
+  return hrm::launch_router_np2<128, 4>(logits, logits_dtype, num_tokens, E, k, norm_topk_prob, probs, topk_idx, topk_weight, weight_dtype, stream);
 }
