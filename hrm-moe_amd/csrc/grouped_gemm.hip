@@ -24,6 +24,7 @@
 //    stored as [k][cols] (kr_swz) and read with ds_read_b64_tr_b16, which
 //    transposes 4x16 blocks of 16-bit values inside each 16-lane group.
 #include <stdio.h>
+#include <type_traits>
 #include <stdlib.h>
 
 #include "common.h"
@@ -616,7 +617,9 @@ __global__ __launch_bounds__(NW * 64, 1) void mgemm_dma_kernel(const uint16_t* _
   static_assert(BN == 128 || BN == 256, "BN is 128 or 256");
   static_assert(A_INSTR >= 1 && B_INSTR >= 1 && NB >= 1 && (KIND != KIND_GATHER_SWIGLU || NB % 2 == 0), "tile split");
   static_assert(STAGES >= 2 && STAGES <= 5, "2..5 stages");
-  static_assert(STAGES * STAGE_BYTES <= 160 * 1024, "LDS ring exceeds 160 KB");
+  // the ring plus the tile plan (3 ints per expert, dynamic) must fit one
+  // workgroup's 160 KB of LDS, or the dispatch is rejected
+  static_assert(STAGES * STAGE_BYTES + 3 * 4 * kMaxExperts <= 160 * 1024, "LDS budget exceeds 160 KB");
   __shared__ __attribute__((aligned(1024))) char smem[STAGES * STAGE_BYTES];
   extern __shared__ int plan_lds[];  // [3][E]: row start, row end, inclusive M-tile prefix
 
@@ -731,7 +734,14 @@ __global__ __launch_bounds__(NW * 64, 1) void mgemm_dma_kernel(const uint16_t* _
   auto take_prefetched = [&]() __attribute__((always_inline)) {
     // tile metadata is wave-uniform: keep it in SGPRs so descriptors built from
     // it need no per-lane (waterfall) handling
-    const int nt = __builtin_amdgcn_readfirstlane(pf_t - (pf_t / tiles_n) * tiles_n);
+    // N tile of list entry pf_t, rotated by mt * tiles_n / nloc: a workgroup
+    // walks the list with stride nloc, i.e. nloc / tiles_n M tiles per step,
+    // so the rotation advances by one N tile per step and every workgroup sees
+    // each N tile equally often (the gate/up kernel's last N tile may be a
+    // cheaper half tile).
+    const int mt_ = pf_t / tiles_n;
+    const int rot = (int)(((int64_t)mt_ * tiles_n) / nloc);
+    const int nt = __builtin_amdgcn_readfirstlane((pf_t - mt_ * tiles_n + rot) % tiles_n);
     iss_rs = __builtin_amdgcn_readfirstlane(pf_m.row_start);
     iss_re = __builtin_amdgcn_readfirstlane(pf_m.row_end);
     const int ex = __builtin_amdgcn_readfirstlane(pf_m.expert);
@@ -815,12 +825,22 @@ __global__ __launch_bounds__(NW * 64, 1) void mgemm_dma_kernel(const uint16_t* _
   for (int s2 = 0; s2 < STAGES - 1; ++s2) issue_next();
 
   int g0 = 0;  // global index of the computing tile's step 0
-  while (true) {
-    floatx16 acc[NB][MB];
+
+  // One tile: K loop and epilogue.  A "half" tile (gate/up kernel with 8 waves
+  // and 256-row weight tiles, when at most 64 gate columns remain) puts the 8
+  // waves on a 4 x 2 grid of 64 rows x (32 gate + 32 up) columns, so the last
+  // N tile of a width that is an odd multiple of 64 keeps every wave busy on
+  // valid columns.  Its B tile rows past the valid ones are loaded but unused.
+  auto tile = [&](auto half_tag) __attribute__((always_inline)) {
+    constexpr bool H = decltype(half_tag)::value;
+    constexpr int MBH = H ? 2 : MB;                               // 32-row blocks per wave
+    const int row_base = H ? (wave >> 1) * 64 : wm * (BM / 2);    // first tile row of this wave
+    const int col_blk = H ? (wave & 1) * 32 : wn * (BN / 2 / WGN);  // gate/up column block (gate/up kernel)
+    floatx16 acc[NB][MBH];
 #pragma unroll
     for (int b = 0; b < NB; ++b)
 #pragma unroll
-      for (int a = 0; a < MB; ++a)
+      for (int a = 0; a < MBH; ++a)
 #pragma unroll
         for (int v = 0; v < 16; ++v) acc[b][a][v] = 0.0f;
 
@@ -831,21 +851,21 @@ __global__ __launch_bounds__(NW * 64, 1) void mgemm_dma_kernel(const uint16_t* _
       if (issued == gs + STAGES - 1) issue_next();
       const char* la = smem + (gs % STAGES) * STAGE_BYTES;
       const char* lb = la + A_BYTES;
-      u32x4 fw[2][NB], fa[2][MB];
-      auto load_frags = [&](int s, u32x4 (&w)[NB], u32x4 (&x)[MB]) __attribute__((always_inline)) {
+      u32x4 fw[2][NB], fa[2][MBH];
+      auto load_frags = [&](int s, u32x4 (&w)[NB], u32x4 (&x)[MBH]) __attribute__((always_inline)) {
 #pragma unroll
         for (int b = 0; b < NB; ++b) {
           int r0;
           if constexpr (KIND == KIND_GATHER_SWIGLU)  // gate blocks, then the matching up blocks
-            r0 = (b < NB / 2 ? 0 : BN / 2) + wn * (BN / 2 / WGN) + (b % (NB / 2)) * 32;
+            r0 = (b < NB / 2 ? 0 : BN / 2) + col_blk + (b % (NB / 2)) * 32;
           else
             r0 = wn * (BN / WGN) + b * 32;
           if constexpr (KIND == KIND_NN) w[b] = tr_operand<BN>(lb, r0, s, lane);
           else w[b] = lds_read16(lb, kcp_off<PK>(r0 + (lane & 31), s * 2 + (lane >> 5)));
         }
 #pragma unroll
-        for (int a = 0; a < MB; ++a)
-          x[a] = lds_read16(la, kcp_off<PK>(wm * (BM / 2) + a * 32 + (lane & 31), s * 2 + (lane >> 5)));
+        for (int a = 0; a < MBH; ++a)
+          x[a] = lds_read16(la, kcp_off<PK>(row_base + a * 32 + (lane & 31), s * 2 + (lane >> 5)));
       };
       load_frags(0, fw[0], fa[0]);
 #pragma unroll
@@ -854,7 +874,7 @@ __global__ __launch_bounds__(NW * 64, 1) void mgemm_dma_kernel(const uint16_t* _
 #pragma unroll
         for (int b = 0; b < NB; ++b)
 #pragma unroll
-          for (int a = 0; a < MB; ++a) acc[b][a] = TR::mfma32(fw[s & 1][b], fa[s & 1][a], acc[b][a]);
+          for (int a = 0; a < MBH; ++a) acc[b][a] = TR::mfma32(fw[s & 1][b], fa[s & 1][a], acc[b][a]);
       }
     }
 
@@ -868,55 +888,63 @@ __global__ __launch_bounds__(NW * 64, 1) void mgemm_dma_kernel(const uint16_t* _
     const int c_rs = __builtin_amdgcn_readfirstlane(comp_rs);
     const int c_rows = __builtin_amdgcn_readfirstlane(comp_re - comp_rs);
     const __amdgpu_buffer_rsrc_t rC = make_rsrc(C + (int64_t)c_rs * N, (uint32_t)c_rows * (uint32_t)N * 2);
-    {
-      constexpr int WCOLS = KIND == KIND_GATHER_SWIGLU ? BN / 2 / WGN : BN / WGN;  // output columns per wave
-      constexpr int PITCH = WCOLS * 2;                                      // staged row bytes
-      constexpr int C8 = PITCH / 8;                                         // 8-byte chunks per row
-      constexpr int RP = 256 / PITCH;                                       // rows per 256 bytes
-      constexpr int REGION = STAGE_BYTES / NW;                              // staging bytes per wave
-      constexpr int FIT = REGION / (32 * PITCH);                            // 32-row blocks that fit
-      constexpr int APP = FIT >= 4 && MB >= 4 ? 4 : (FIT >= 2 && MB >= 2 ? 2 : 1);  // blocks per pass
-      constexpr int LPR = PITCH / 16;                                       // read-back lanes per row
-      constexpr int RPI = 64 / LPR;                                         // rows per read-back
-      static_assert(FIT >= 1 && MB % APP == 0 && RP * C8 == 32, "staging layout");
-      char* stg = smem + ((g0 + nk - 1) % STAGES) * STAGE_BYTES + wave * REGION;
-      const int col0 = comp_n0 + wn * WCOLS;
-      barrier_lds();
+    constexpr int WCOLS = KIND == KIND_GATHER_SWIGLU ? BN / 2 / WGN : BN / WGN;  // output columns per wave
+    constexpr int PITCH = WCOLS * 2;                                      // staged row bytes
+    constexpr int C8 = PITCH / 8;                                         // 8-byte chunks per row
+    constexpr int RP = 256 / PITCH;                                       // rows per 256 bytes
+    constexpr int REGION = STAGE_BYTES / NW;                              // staging bytes per wave
+    constexpr int FIT = REGION / (32 * PITCH);                            // 32-row blocks that fit
+    constexpr int APP = FIT >= 4 && MBH >= 4 ? 4 : (FIT >= 2 && MBH >= 2 ? 2 : 1);  // blocks per pass
+    constexpr int LPR = PITCH / 16;                                       // read-back lanes per row
+    constexpr int RPI = 64 / LPR;                                         // rows per read-back
+    static_assert(FIT >= 1 && MBH % APP == 0 && RP * C8 == 32, "staging layout");
+    char* stg = smem + ((g0 + nk - 1) % STAGES) * STAGE_BYTES + wave * REGION;
+    const int col0 = comp_n0 + (KIND == KIND_GATHER_SWIGLU ? col_blk : wn * WCOLS);
+    barrier_lds();
 #pragma unroll
-      for (int a0 = 0; a0 < MB; a0 += APP) {
+    for (int a0 = 0; a0 < MBH; a0 += APP) {
 #pragma unroll
-        for (int a = a0; a < a0 + APP; ++a) {
-          const int r = (a - a0) * 32 + (lane & 31);
-          const int g = (r / RP) % C8;
+      for (int a = a0; a < a0 + APP; ++a) {
+        const int r = (a - a0) * 32 + (lane & 31);
+        const int g = (r / RP) % C8;
 #pragma unroll
-          for (int b = 0; b < WCOLS / 32; ++b)
+        for (int b = 0; b < WCOLS / 32; ++b)
 #pragma unroll
-            for (int gq = 0; gq < 4; ++gq) {
-              float o[4];
+          for (int gq = 0; gq < 4; ++gq) {
+            float o[4];
 #pragma unroll
-              for (int q = 0; q < 4; ++q) {
-                if constexpr (KIND == KIND_GATHER_SWIGLU)
-                  o[q] = swiglu_fast<TR>(acc[b][a][gq * 4 + q], acc[b + NB / 2][a][gq * 4 + q]);
-                else
-                  o[q] = acc[b][a][gq * 4 + q];
-              }
-              const int ch8 = (b * 32 + gq * 8) / 4 + (lane >> 5);
-              *reinterpret_cast<u32x2*>(stg + r * PITCH + ((ch8 ^ g) << 3)) = pack4<TR>(o[0], o[1], o[2], o[3]);
+            for (int q = 0; q < 4; ++q) {
+              if constexpr (KIND == KIND_GATHER_SWIGLU)
+                o[q] = swiglu_fast<TR>(acc[b][a][gq * 4 + q], acc[b + NB / 2][a][gq * 4 + q]);
+              else
+                o[q] = acc[b][a][gq * 4 + q];
             }
-        }
-#pragma unroll
-        for (int i = 0; i < APP * 32 / RPI; ++i) {
-          const int r = i * RPI + lane / LPR;
-          const int c16 = lane % LPR;
-          const int g = (r / RP) % C8;
-          u32x4 v = *reinterpret_cast<const u32x4*>(stg + r * PITCH + ((c16 ^ (g >> 1)) << 4));
-          if (g & 1) v = u32x4{v[2], v[3], v[0], v[1]};
-          const uint32_t ml = (uint32_t)(wm * (BM / 2) + a0 * 32 + r);
-          const int c = col0 + c16 * 8;
-          const uint32_t voff = c < N ? (ml * (uint32_t)N + (uint32_t)c) * 2 : 0x80000000u;
-          bstore16(rC, voff, v);
-        }
+            const int ch8 = (b * 32 + gq * 8) / 4 + (lane >> 5);
+            *reinterpret_cast<u32x2*>(stg + r * PITCH + ((ch8 ^ g) << 3)) = pack4<TR>(o[0], o[1], o[2], o[3]);
+          }
       }
+#pragma unroll
+      for (int i = 0; i < APP * 32 / RPI; ++i) {
+        const int r = i * RPI + lane / LPR;
+        const int c16 = lane % LPR;
+        const int g = (r / RP) % C8;
+        u32x4 v = *reinterpret_cast<const u32x4*>(stg + r * PITCH + ((c16 ^ (g >> 1)) << 4));
+        if (g & 1) v = u32x4{v[2], v[3], v[0], v[1]};
+        const uint32_t ml = (uint32_t)(row_base + a0 * 32 + r);
+        const int c = col0 + c16 * 8;
+        const uint32_t voff = c < N ? (ml * (uint32_t)N + (uint32_t)c) * 2 : 0x80000000u;
+        bstore16(rC, voff, v);
+      }
+    }
+  };
+
+  constexpr bool HALF_OK = KIND == KIND_GATHER_SWIGLU && NW == 8 && BN == 256 && NB == 2;
+  while (true) {
+    if constexpr (HALF_OK) {
+      if (N - comp_n0 <= BN / 4) tile(std::true_type{});
+      else tile(std::false_type{});
+    } else {
+      tile(std::false_type{});
     }
 
     g0 += nk;
@@ -1114,12 +1142,14 @@ int launch_mgemm_dma(const void* A, const int32_t* gather, const void* W, const 
 // Tile shape, pipeline depth, waves and K step of the DMA kernels.
 // Default: 256 x 256 tiles with 8 waves (2 per SIMD, 128 x 64 per wave) and 2
 // stages of 64-wide K steps (128 KB of LDS) when experts average at least 256
-// rows and the weight rows split into whole 256-row tiles; otherwise 128 x 128
+// rows and the weight rows split into whole 256-row tiles (not used for the
+// gate/up kernel by default; it supports a last half tile of 64 gate + 64 up
+// rows when selected explicitly); otherwise 128 x 128
 // tiles, 4 waves, 2 stages (64 KB of LDS, two workgroups per CU).  The large
 // tile halves LDS and L2 traffic per flop; the small one wastes less on ragged
 // experts and on widths that are not multiples of 256.
 // HRM_MOE_GEMM_CFG="<rows>x<cols>x<stages>x<waves>x<kstep>" (e.g.
-// "256x256x5x8x32") overrides the choice with one of the built variants.
+// "256x256x4x8x32") overrides the choice with one of the built variants.
 struct MCfg {
   int bm, bn, stages, waves, bk;
 };
@@ -1127,17 +1157,20 @@ bool mcfg_built(const MCfg& c) {
   if (c.bm == 128 && c.bn == 128 && c.waves == 4)
     return (c.bk == 64 && (c.stages == 2 || c.stages == 3)) || (c.bk == 32 && (c.stages == 4 || c.stages == 5));
   if (c.bm == 256 && c.bn == 256 && c.waves == 8)
-    return (c.bk == 64 && c.stages == 2) || (c.bk == 32 && (c.stages == 4 || c.stages == 5));
+    return (c.bk == 64 && c.stages == 2) || (c.bk == 32 && c.stages == 4);
   return false;
 }
-MCfg mgemm_cfg(int64_t M, int E, int64_t w_rows) {
-  static const char* env = getenv("HRM_MOE_GEMM_CFG");
-  if (env) {
+MCfg mgemm_cfg(int64_t M, int E, int64_t w_rows, bool gate_up) {
+  const char* env = getenv("HRM_MOE_GEMM_CFG");  // read per call: tests switch variants in one process
+  if (env && *env) {
     MCfg c{0, 0, 0, 4, 64};
     const int n = sscanf(env, "%dx%dx%dx%dx%d", &c.bm, &c.bn, &c.stages, &c.waves, &c.bk);
     if (n >= 3 && mcfg_built(c)) return c;
   }
-  if (M >= (int64_t)E * 256 && w_rows % 256 == 0) return MCfg{256, 256, 2, 8, 64};
+  // The gate/up kernel stays on 128 x 128 tiles: its gathered rows measured
+  // slower per cycle on 256 x 256 tiles even with half tiles balancing the
+  // last N tile.
+  if (!gate_up && M >= (int64_t)E * 256 && w_rows % 256 == 0) return MCfg{256, 256, 2, 8, 64};
   return MCfg{128, 128, 2, 4, 64};
 }
 
@@ -1153,7 +1186,7 @@ int dispatch_mgemm_t(const void* A, const int32_t* gather, const void* W, const 
                                  : launch_mgemm<TR, KIND, 128, 128>(A, gather, W, tpe, M, N, K, E, C, workspace, stream);
   }
   // weight rows spanned by the N tiles: 2N for the gate/up pair, else N
-  MCfg c = mgemm_cfg(M, E, KIND == KIND_GATHER_SWIGLU ? 2 * (int64_t)N : (int64_t)N);
+  MCfg c = mgemm_cfg(M, E, KIND == KIND_GATHER_SWIGLU ? 2 * (int64_t)N : (int64_t)N, KIND == KIND_GATHER_SWIGLU);
   if (K % c.bk != 0) c = MCfg{128, 128, 2, 4, 64};
   // the ring may run at most one tile ahead: STAGES - 1 <= K / BK
   if (c.stages - 1 > K / c.bk) {
@@ -1163,10 +1196,7 @@ int dispatch_mgemm_t(const void* A, const int32_t* gather, const void* W, const 
 #define HRM_MG(BM_, BN_, ST_, NW_, BK_) \
   return launch_mgemm_dma<TR, KIND, BM_, BN_, ST_, NW_, BK_>(A, gather, W, tpe, M, N, K, E, a_rows, C, workspace, stream)
   if (c.bm == 256) {
-    if (c.bk == 32) {
-      if (c.stages == 5) HRM_MG(256, 256, 5, 8, 32);
-      HRM_MG(256, 256, 4, 8, 32);
-    }
+    if (c.bk == 32) HRM_MG(256, 256, 4, 8, 32);
     HRM_MG(256, 256, 2, 8, 64);
   }
   if (c.bk == 32) {
