@@ -13,7 +13,7 @@ roofline of the dominant kernel (fused gate_up + SwiGLU GEMM, timed with
 events on its stream during the timed steps) and the reference's eager CPU
 path timed on the host's cores over a bounded sample.
 
-Usage: python bench.py [--steps K] [--warmup W] [--gpus 1] [--workload l64x8|xl_skew|xl128]
+Usage: python bench.py [--steps K] [--warmup W] [--gpus 1] [--workload l64x8|xl_skew|xl128|decode_t{1,8,64,256}]
        python bench.py --calibrate-copy-mb 512   (a plain copy, for scaling rocprofv3 byte counters)
 """
 from __future__ import annotations
@@ -39,6 +39,11 @@ WORKLOADS = {
     "l64x8": (16384, 1280, 64, 448, 8, 0.0),
     "xl_skew": (16384, 1536, 64, 512, 8, 1.5),
     "xl128": (32768, 1536, 128, 512, 8, 0.0),
+    # decode steps of the XL 64x8 layer: HBM-bound weight streaming, replayed from a HIP graph
+    "decode_t1": (1, 1536, 64, 512, 8, 0.0),
+    "decode_t8": (8, 1536, 64, 512, 8, 0.0),
+    "decode_t64": (64, 1536, 64, 512, 8, 0.0),
+    "decode_t256": (256, 1536, 64, 512, 8, 0.0),
 }
 
 
@@ -171,8 +176,68 @@ def cpu_baseline(t, h, e, i, k, sample_tokens=2048, runs=5):
         "sample": (f"{sample_tokens} of {t} tokens of the same layer shape, bf16, reference eager CPU path "
                    f"(per-expert F.linear), median of {runs} runs after 1 warmup: {sec * 1e3:.1f} ms; "
                    f"os.cpu_count()={os.cpu_count()}, affinity={affinity}"),
-        "ms_per_layer_extrapolated": round(sec * 1e3 * t / sample_tokens, 1),
+        "ms_per_layer_extrapolated": round(sec * 1e3 * t / sample_tokens, 4),
     }
+
+
+def run_decode(args, hrm, dev):
+    """Decode-size layer latency: graph replays rotating over weight copies that together exceed the MALL."""
+    from hrm_moe_amd import ops
+
+    t, h, e, i, k, _ = WORKLOADS[args.workload]
+    copies = max(args.weight_copies, 8)
+    layers, xs, graphs = [], [], []
+    for c in range(copies):
+        layer, x = make_layer(hrm, dev, t, h, e, i, k, 0.0, seed=4321 + c)
+        layers.append(layer)
+        xs.append(x)
+        graphs.append(hrm.GraphedMoEForward(layer, x))
+    for s in range(args.warmup):
+        graphs[s % copies](xs[s % copies])
+    torch.cuda.synchronize()
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    start.record()
+    for s in range(args.steps):
+        graphs[s % copies](xs[s % copies])
+    end.record()
+    torch.cuda.synchronize()
+    us = start.elapsed_time(end) / args.steps * 1e3
+    # algorithmic bytes: the touched experts' weights, the tokens in and out, the router weight
+    with torch.no_grad():
+        distinct = []
+        for c in range(copies):
+            logits = torch.nn.functional.linear(xs[c], layers[c].gate.weight)
+            distinct.append(int(torch.unique(ops.router_topk(logits, k, True, torch.bfloat16)[2]).numel()))
+    touched = statistics.fmean(distinct)
+    nbytes = touched * 3 * h * i * 2 + 2 * t * h * 2 + h * e * 2
+    gbs = nbytes / (us * 1e-6) / 1e9
+    log(f"decode T={t}: {us:.2f} us/layer, {touched:.1f} experts touched, {nbytes / 1e6:.1f} MB, {gbs:.0f} GB/s")
+    result = {
+        "metric": f"MoE FFN decode latency, XL 64x8 (H={h}, E={e}, I={i}, top-{k}), {t} tokens",
+        "value": round(us, 3),
+        "unit": "us/layer",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(us / 1e3, 6),
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {"workload": f"{args.workload}: MoE FFN layer forward replayed from a HIP graph, {t} tokens, "
+                               f"H={h}, E={e}, I={i}, top-{k}, {copies} weight copies",
+                   "tokens": t, "hidden": h, "experts": e, "inter": i, "top_k": k, "weight_copies": copies},
+        "roofline": {"kernel": "whole layer (weight streaming)", "bound": "hbm", "achieved": round(gbs, 1),
+                     "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": None,
+                     "bytes_per_step": int(nbytes), "experts_touched": touched},
+    }
+    if not args.no_cpu_baseline:
+        cb = cpu_baseline(t, h, e, i, k, sample_tokens=t, runs=5)
+        result["cpu_baseline"] = {"value": round(cb["ms_per_layer_extrapolated"] * 1e3, 1), "unit": "us/layer",
+                                  "cores": cb["cores"], "kind": cb["kind"], "sample": cb["sample"]}
+    print(json.dumps(result), flush=True)
 
 
 def main():
@@ -197,6 +262,9 @@ def main():
 
     hrm.load_library()
     dev = torch.device("cuda:0")
+    if args.workload.startswith("decode"):
+        run_decode(args, hrm, dev)
+        return
     t, h, e, i, k, bias = WORKLOADS[args.workload]
     r = t * k
     layers, xs = [], []

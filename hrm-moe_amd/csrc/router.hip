@@ -62,10 +62,14 @@ __device__ __forceinline__ void select_round(uint32_t (&key)[C], int e0, uint32_
   int be = 0x7fffffff;
 #pragma unroll
   for (int j = 0; j < C; ++j) {
-    if (key[j] > bk) { bk = key[j]; be = e0 + j; }
+    const bool b = key[j] > bk;
+    bk = b ? key[j] : bk;
+    be = b ? e0 + j : be;
   }
   auto merge = [&](uint32_t ok, int oe) __attribute__((always_inline)) {
-    if (ok > bk || (ok == bk && oe < be)) { bk = ok; be = oe; }
+    const bool b = ok > bk || (ok == bk && oe < be);
+    bk = b ? ok : bk;
+    be = b ? oe : be;
   };
   if constexpr (LPR == 16) {
     merge(xlane<8>(bk), (int)xlane<8>((uint32_t)be));
@@ -74,20 +78,21 @@ __device__ __forceinline__ void select_round(uint32_t (&key)[C], int e0, uint32_
   merge(xlane<2>(bk), (int)xlane<2>((uint32_t)be));
   merge(xlane<1>(bk), (int)xlane<1>((uint32_t)be));
 #pragma unroll
-  for (int j = 0; j < C; ++j) {
-    if (e0 + j == be) key[j] = 0u;
-  }
+  for (int j = 0; j < C; ++j) key[j] = (e0 + j == be) ? 0u : key[j];
   out_key = bk;
   out_idx = be;
 }
 
-template <int NP2, int SLOTS, int LPR>
+// KFIX: k == SLOTS, known at compile time (the usual top-2/4/8).
+template <int NP2, int SLOTS, int LPR, bool KFIX>
 __global__ __launch_bounds__(256) void router_topk_kernel(const void* __restrict__ logits, int ldt, int64_t T, int E,
-                                                          int k, int norm, float* __restrict__ probs,
+                                                          int k_rt, int norm, float* __restrict__ probs,
                                                           int64_t* __restrict__ idx_out, void* __restrict__ w_out,
                                                           int wdt) {
   constexpr int C = NP2 / LPR;
   constexpr int RPB = 256 / LPR;  // rows per block
+  constexpr int KC = KFIX ? SLOTS : 0;
+  const int k = KFIX ? SLOTS : k_rt;
   static_assert(LPR == 4 || LPR == 16, "4 or 16 lanes per row");
   static_assert(C >= 1 && (C & (C - 1)) == 0, "experts per lane");
   const int q = threadIdx.x % LPR;
@@ -98,14 +103,35 @@ __global__ __launch_bounds__(256) void router_topk_kernel(const void* __restrict
 
   float s[C];
   float mx = -INFINITY;
+  // Loads use a clamped (always valid) address and a select instead of a
+  // branch per element.  With E a multiple of 8, 16-bit logits come in as
+  // 16-byte vectors, each wholly inside or wholly outside the row.
+  const int64_t rr = active ? row : T - 1;
+  if (ldt != HRM_MOE_F32 && (E % 8) == 0 && (C % 8) == 0) {
+    const uint16_t* base = reinterpret_cast<const uint16_t*>(logits) + rr * E;
 #pragma unroll
-  for (int j = 0; j < C; ++j) {
-    const int e = e0 + j;
-    float x = -INFINITY;
-    if (active && e < E) x = load_logit(logits, ldt, row * E + e);
-    s[j] = x;
-    mx = fmaxf(mx, x);
+    for (int v = 0; v < C / 8; ++v) {
+      const int ev = e0 + v * 8;
+      const bool in = active && ev < E;
+      const u32x4 raw = *reinterpret_cast<const u32x4*>(base + (in ? ev : 0));
+#pragma unroll
+      for (int q2 = 0; q2 < 8; ++q2) {
+        const uint16_t h = (uint16_t)(q2 & 1 ? raw[q2 >> 1] >> 16 : raw[q2 >> 1] & 0xffffu);
+        const float f = ldt == HRM_MOE_BF16 ? BF16::to_f(h) : F16::to_f(h);
+        s[v * 8 + q2] = in ? f : -INFINITY;
+      }
+    }
+  } else {
+#pragma unroll
+    for (int j = 0; j < C; ++j) {
+      const int e = e0 + j;
+      const bool in = active && e < E;
+      const float f = load_logit(logits, ldt, rr * E + (in ? e : 0));
+      s[j] = in ? f : -INFINITY;
+    }
   }
+#pragma unroll
+  for (int j = 0; j < C; ++j) mx = fmaxf(mx, s[j]);
   if constexpr (LPR == 16) {
     mx = fmaxf(mx, xlanef<8>(mx));
     mx = fmaxf(mx, xlanef<4>(mx));
@@ -161,12 +187,12 @@ __global__ __launch_bounds__(256) void router_topk_kernel(const void* __restrict
     if (!active) return;
     uint32_t gk[SLOTS];
     int gi[SLOTS];
-    torch_topk_order<SLOTS>(sk, si, k, gk, gi);
+    torch_topk_order<SLOTS, KC>(sk, si, k, gk, gi);
     float w[SLOTS];
 #pragma unroll
     for (int j = 0; j < SLOTS; ++j) w[j] = __uint_as_float(gk[j] - 1u);
     if (norm) {
-      float sum = torch_row_sum<SLOTS>(w, k);
+      float sum = torch_row_sum<SLOTS, KC>(w, k);
       sum = (sum != sum) ? sum : fmaxf(sum, 1e-12f);
 #pragma unroll
       for (int j = 0; j < SLOTS; ++j) w[j] = w[j] / sum;
@@ -215,15 +241,18 @@ int launch_router_np2(const void* logits, int ldt, int64_t T, int E, int k, int 
                       void* w, int wdt, void* stream) {
   constexpr int RPB = 256 / LPR;
   dim3 grid((unsigned)((T + RPB - 1) / RPB)), block(256);
-#define HRM_RT(SL) \
-  HRM_LAUNCH((router_topk_kernel<NP2, SL, LPR>), grid, block, 0, stream, logits, ldt, T, E, k, norm, probs, idx, w, wdt)
-  if (k <= 2) HRM_RT(2);
-  else if (k <= 4) HRM_RT(4);
-  else if (k <= 8) HRM_RT(8);
+#define HRM_RT(SL, KF) \
+  HRM_LAUNCH((router_topk_kernel<NP2, SL, LPR, KF>), grid, block, 0, stream, logits, ldt, T, E, k, norm, probs, idx, w, wdt)
+  if (k == 2) HRM_RT(2, true);
+  else if (k == 4) HRM_RT(4, true);
+  else if (k == 8) HRM_RT(8, true);
+  else if (k <= 2) HRM_RT(2, false);
+  else if (k <= 4) HRM_RT(4, false);
+  else if (k <= 8) HRM_RT(8, false);
   else if constexpr (NP2 >= 16) {
-    if (k <= 16) HRM_RT(16);
+    if (k <= 16) HRM_RT(16, false);
     else if constexpr (NP2 >= 32) {
-      HRM_RT(32);
+      HRM_RT(32, false);
     } else {
       return HRM_MOE_ERR_UNSUPPORTED;
     }

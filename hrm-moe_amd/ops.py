@@ -49,8 +49,8 @@ def router_topk(logits: torch.Tensor, top_k: int, norm_topk_prob: bool, weight_d
     probs = torch.empty((t, e), dtype=torch.float32, device=dev) if want_probs else None
     idx = torch.empty((t, top_k), dtype=torch.int64, device=dev)
     w = torch.empty((t, top_k), dtype=weight_dtype, device=dev)
-    with torch.cuda.device(dev):
-        st = _lib.load().hrm_moe_router_topk(
+    with _lib.device_guard(dev):
+        st = _lib.lib().hrm_moe_router_topk(
             _lib.ptr(logits), _lib.dtype_code(logits.dtype), t, e, top_k, int(bool(norm_topk_prob)), _lib.ptr(probs),
             _lib.ptr(idx), _lib.ptr(w), _lib.dtype_code(weight_dtype), _lib.stream_of(dev))
     _lib.check(st, "router_topk")
@@ -78,7 +78,7 @@ def permute(topk_idx: torch.Tensor, num_experts: int, want_sort_idx: bool = Fals
     topk_idx = topk_idx.to(torch.int64).contiguous()
     t, k = topk_idx.shape
     r = t * k
-    lib = _lib.load()
+    lib = _lib.lib()
     tpe = torch.empty(num_experts, dtype=torch.int64, device=dev)
     offs = torch.empty(num_experts + 1, dtype=torch.int32, device=dev)
     sti = torch.empty(r, dtype=torch.int32, device=dev)
@@ -88,7 +88,7 @@ def permute(topk_idx: torch.Tensor, num_experts: int, want_sort_idx: bool = Fals
     if ws_bytes == 0:
         _lib.check(_lib.ERR_UNSUPPORTED if num_experts > 1024 else _lib.ERR_INVALID, "permute")
     ws = _workspace(ws_bytes, dev)
-    with torch.cuda.device(dev):
+    with _lib.device_guard(dev):
         st = lib.hrm_moe_permute(_lib.ptr(topk_idx), t, num_experts, k, _lib.ptr(tpe), _lib.ptr(offs), _lib.ptr(sti),
                                  _lib.ptr(sidx), _lib.ptr(s2r), _lib.ptr(ws), ws.numel(), _lib.stream_of(dev))
     _lib.check(st, "permute")
@@ -124,9 +124,9 @@ def grouped_gemm_nt(a: torch.Tensor, w: torch.Tensor, tokens_per_expert: torch.T
     if tpe.numel() != e:
         raise ValueError(f"tokens_per_expert has {tpe.numel()} entries for {e} experts")
     c = a.new_empty((m, n))
-    lib = _lib.load()
+    lib = _lib.lib()
     ws = _workspace(lib.hrm_moe_grouped_gemm_workspace_size(m, e), dev)
-    with torch.cuda.device(dev):
+    with _lib.device_guard(dev):
         st = lib.hrm_moe_grouped_gemm_nt(_lib.ptr(a), _lib.ptr(w), _lib.ptr(tpe), m, n, k, e, dt, _lib.ptr(c),
                                          _lib.ptr(ws), ws.numel(), _lib.stream_of(dev))
     _lib.check(st, "grouped_gemm_nt")
@@ -148,9 +148,9 @@ def grouped_gemm_nn(a: torch.Tensor, w: torch.Tensor, tokens_per_expert: torch.T
     if tpe.numel() != e:
         raise ValueError(f"tokens_per_expert has {tpe.numel()} entries for {e} experts")
     c = a.new_empty((m, n))
-    lib = _lib.load()
+    lib = _lib.lib()
     ws = _workspace(lib.hrm_moe_grouped_gemm_workspace_size(m, e), dev)
-    with torch.cuda.device(dev):
+    with _lib.device_guard(dev):
         st = lib.hrm_moe_grouped_gemm_nn(_lib.ptr(a), _lib.ptr(w), _lib.ptr(tpe), m, n, k, e, dt, _lib.ptr(c),
                                          _lib.ptr(ws), ws.numel(), _lib.stream_of(dev))
     _lib.check(st, "grouped_gemm_nn")
@@ -171,9 +171,9 @@ def grouped_gemm_tn(a: torch.Tensor, b: torch.Tensor, tokens_per_expert: torch.T
     tpe = _tpe64(tokens_per_expert, dev)
     e = tpe.numel()
     c = a.new_empty((e, na, nb))
-    lib = _lib.load()
+    lib = _lib.lib()
     ws = _workspace(lib.hrm_moe_grouped_gemm_workspace_size(m, e), dev)
-    with torch.cuda.device(dev):
+    with _lib.device_guard(dev):
         st = lib.hrm_moe_grouped_gemm_tn(_lib.ptr(a), _lib.ptr(b), _lib.ptr(tpe), m, na, nb, e, dt, _lib.ptr(c),
                                          _lib.ptr(ws), ws.numel(), _lib.stream_of(dev))
     _lib.check(st, "grouped_gemm_tn")
@@ -198,9 +198,9 @@ def gate_up_swiglu(hidden: torch.Tensor, dispatch: Dispatch, gate_up_weight: tor
     hidden, gate_up_weight = hidden.contiguous(), gate_up_weight.contiguous()
     r = dispatch.sorted_token_idx.numel()
     act = hidden.new_empty((r, inter))
-    lib = _lib.load()
+    lib = _lib.lib()
     ws = _workspace(lib.hrm_moe_grouped_gemm_workspace_size(r, e), dev)
-    with torch.cuda.device(dev):
+    with _lib.device_guard(dev):
         st = lib.hrm_moe_gate_up_swiglu(_lib.ptr(hidden), _lib.ptr(dispatch.sorted_token_idx),
                                         _lib.ptr(dispatch.tokens_per_expert), _lib.ptr(gate_up_weight), t, r, h, inter,
                                         e, dt, _lib.ptr(act), _lib.ptr(ws), ws.numel(), _lib.stream_of(dev))
@@ -220,8 +220,8 @@ def combine(expert_out: torch.Tensor, dispatch: Dispatch, topk_weight: torch.Ten
     expert_out, topk_weight = expert_out.contiguous(), topk_weight.contiguous()
     e = dispatch.tokens_per_expert.numel()
     out = expert_out.new_empty((t, h))
-    with torch.cuda.device(dev):
-        st = _lib.load().hrm_moe_combine(_lib.ptr(expert_out), _lib.ptr(dispatch.slot_to_row), _lib.ptr(topk_weight),
+    with _lib.device_guard(dev):
+        st = _lib.lib().hrm_moe_combine(_lib.ptr(expert_out), _lib.ptr(dispatch.slot_to_row), _lib.ptr(topk_weight),
                                          _lib.ptr(dispatch.expert_offsets), t, k, h, e,
                                          _lib.dtype_code(expert_out.dtype), _lib.ptr(out), _lib.stream_of(dev))
     _lib.check(st, "combine")

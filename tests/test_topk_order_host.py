@@ -55,6 +55,18 @@ def test_ordering_matches_oracle_for_every_k(checker, k, loop_form):
         assert np.array_equal(got_sum, reg_sum)
 
 
+@pytest.mark.parametrize("k", [2, 4, 8, 16, 32])
+def test_compile_time_k_form_matches_oracle(checker, k):
+    """The router's k == SLOTS specialisation (k fixed at compile time)."""
+    rng = np.random.default_rng(100 + k)
+    vals = (rng.integers(0, 4, size=(600, 64)).astype(np.float32) * 0.125 + 0.0625)
+    got, got_sum = run_checker(checker, vals, k, 2)
+    _, want = mo.topk_rocm(vals, k)
+    assert np.array_equal(got, want)
+    _, reg_sum = run_checker(checker, vals, k, 0)
+    assert np.array_equal(got_sum, reg_sum)
+
+
 def test_ordering_matches_device_fixture(checker):
     d = np.load(os.path.join(HERE, "golden", "topk_ties_rocm.npz"))
     for case in ("e64_k8_l4", "e128_k8_l8", "e8_k2_l3", "e8_k3_l3", "e64_k4_l6"):
