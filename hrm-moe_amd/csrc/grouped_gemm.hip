@@ -588,8 +588,10 @@ __device__ __forceinline__ void bstore16(__amdgpu_buffer_rsrc_t r, uint32_t voff
 // Output stores go through a buffer resource covering the tile's rows; lanes
 // with nothing to store get an offset past it, so every wave issues the same
 // stores and no branch is taken.
+// 4-wave variants are sized for two workgroups per CU (at most 256 registers
+// per lane, two waves per SIMD); 8-wave variants run one per CU.
 template <typename TR, int KIND, int BM, int BN, int STAGES, int NW, int BK>
-__global__ __launch_bounds__(NW * 64, 1) void mgemm_dma_kernel(const uint16_t* __restrict__ A,
+__global__ __launch_bounds__(NW * 64, NW == 4 ? 2 : 1) void mgemm_dma_kernel(const uint16_t* __restrict__ A,
                                                                const int32_t* __restrict__ gather,
                                                                const uint16_t* __restrict__ W,
                                                                uint16_t* __restrict__ C,
@@ -1154,6 +1156,7 @@ struct MCfg {
   int bm, bn, stages, waves, bk;
 };
 bool mcfg_built(const MCfg& c) {
+  if (c.bm == 256 && c.bn == 128 && c.waves == 4) return c.bk == 32 && (c.stages == 2 || c.stages == 3);
   if (c.bm == 128 && c.bn == 128 && c.waves == 4)
     return (c.bk == 64 && (c.stages == 2 || c.stages == 3)) || (c.bk == 32 && (c.stages == 4 || c.stages == 5));
   if (c.bm == 256 && c.bn == 256 && c.waves == 8)
@@ -1195,6 +1198,10 @@ int dispatch_mgemm_t(const void* A, const int32_t* gather, const void* W, const 
   }
 #define HRM_MG(BM_, BN_, ST_, NW_, BK_) \
   return launch_mgemm_dma<TR, KIND, BM_, BN_, ST_, NW_, BK_>(A, gather, W, tpe, M, N, K, E, a_rows, C, workspace, stream)
+  if (c.bm == 256 && c.bn == 128) {
+    if (c.stages == 2) HRM_MG(256, 128, 2, 4, 32);
+    HRM_MG(256, 128, 3, 4, 32);
+  }
   if (c.bm == 256) {
     if (c.bk == 32) HRM_MG(256, 256, 4, 8, 32);
     HRM_MG(256, 256, 2, 8, 64);

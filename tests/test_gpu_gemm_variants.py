@@ -20,7 +20,7 @@ from oracle import synth
 pytestmark = pytest.mark.gpu
 
 VARIANTS = ["128x128x2x4x64", "128x128x3x4x64", "128x128x4x4x32", "128x128x5x4x32",
-            "256x256x2x8x64", "256x256x4x8x32"]
+            "256x128x2x4x32", "256x128x3x4x32", "256x256x2x8x64", "256x256x4x8x32"]
 
 
 def _ragged(seed, m, e):
