@@ -331,7 +331,7 @@ def main():
         "phase_ms": {n: round(v, 5) for n, v in phases.items()},
         "phase_pass_ms_per_layer": round(ms_instr, 5),
         "roofline": {
-            "kernel": "mgemm_dma_kernel<BF16, GATHER_SWIGLU> (fused gather + gate_up GEMM + SwiGLU) + its plan kernel",
+            "kernel": "mgemm_dma_kernel<BF16, GATHER_SWIGLU, 128, 128, 2, 4, 64> (fused gather + gate_up GEMM + SwiGLU)",
             "bound": "mfma",
             "achieved": round(achieved, 2),
             "peak": PEAK_BF16_TFLOPS,
