@@ -109,10 +109,8 @@ __global__ __launch_bounds__(1024) void plan_kernel(const int64_t* __restrict__ 
     t.pad = 0;
     tiles[i] = t;
   }
-  if (tid == 0) {
-    *count = total;
-    *work_counter = 0;
-  }
+  if (tid == 0) *count = total;
+  if (tid < 8) work_counter[tid] = 0;  // one work counter per XCD
 }
 
 struct GemmWs {
@@ -122,6 +120,7 @@ struct GemmWs {
   int* work_counter;
 };
 
+// work_counter points at 8 ints (one per XCD) inside the 256-byte counter block.
 inline size_t gemm_ws_bytes(int64_t M, int E, int bm_min) {
   const int64_t max_tiles = (M + bm_min - 1) / bm_min + E;
   return align256(sizeof(MTile) * (size_t)max_tiles) + align256(sizeof(int) * 4) + align256(sizeof(int) * (E + 1));
@@ -960,6 +959,172 @@ __global__ __launch_bounds__(NW * 64, NW == 4 ? 2 : 1) void mgemm_dma_kernel(con
   wait_vmcnt<0>();
 }
 
+// Wgrad with 8 waves on BA x BB = 256 x 256 tiles of C[e] (128 x 64 per
+// wave), both operands DMA-fed as [64 k][cols] slices of the expert's rows
+// and read transposed.  Tiles are handed out by one atomic counter per XCD
+// over that XCD's contiguous eighth of the (expert, na-tile, nb-tile) list,
+// so an expert's rows stay in few L2s and ragged experts still balance.  The
+// epilogue is staged through the idle ring like the M-grouped kernels'.
+template <typename TR, int BA, int BB, int NW, int STAGES>
+__global__ __launch_bounds__(NW * 64, 1) void wgrad_dma8_kernel(const uint16_t* __restrict__ A,
+                                                                const uint16_t* __restrict__ B,
+                                                                uint16_t* __restrict__ C,
+                                                                const int* __restrict__ row_offsets, int E, int Na,
+                                                                int Nb, int* __restrict__ counters) {
+  constexpr int WGN = NW / 2;
+  constexpr int MB = BA / 64;             // 32-row (na) blocks per wave, 2 waves along na
+  constexpr int NB = BB / WGN / 32;       // 32-column (nb) blocks per wave
+  constexpr int TA_BYTES = kBK * BA * 2;
+  constexpr int TB_BYTES = kBK * BB * 2;
+  constexpr int STAGE_BYTES = TA_BYTES + TB_BYTES;
+  constexpr int RPI_A = 1024 / (BA * 2), RPI_B = 1024 / (BB * 2);  // k rows per 1 KB instruction
+  constexpr int LPR_A = BA / 8, LPR_B = BB / 8;                     // lanes per k row
+  constexpr int KR = kBK / NW;                                       // k rows loaded per wave
+  constexpr int IA = KR / RPI_A, IB = KR / RPI_B;
+  constexpr int PER = IA + IB;
+  static_assert(IA >= 1 && IB >= 1 && NB >= 1, "tile split");
+  static_assert(STAGES * STAGE_BYTES <= 160 * 1024, "LDS ring exceeds 160 KB");
+  __shared__ __attribute__((aligned(1024))) char smem[STAGES * STAGE_BYTES];
+  __shared__ int s_tile;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave / WGN, wn = wave % WGN;
+  const int ta_n = (Na + BA - 1) / BA, tb_n = (Nb + BB - 1) / BB;
+  const int per_e = ta_n * tb_n;
+  const int total = E * per_e;
+  const int xcd = blockIdx.x & 7;
+  const int chunk = (total + 7) >> 3;
+  const int t_begin = xcd * chunk;
+  const int t_end = min(total, t_begin + chunk);
+
+  while (true) {
+    if (tid == 0) s_tile = t_begin + atomicAdd(&counters[xcd], 1);
+    __syncthreads();  // also orders the previous tile's staging reads before this tile's DMA
+    const int t = s_tile;
+    __syncthreads();
+    if (t >= t_end) break;
+    const int e = t / per_e;
+    const int rem = t - e * per_e;
+    const int a0 = (rem / tb_n) * BA, b0 = (rem % tb_n) * BB;
+    const int rs = row_offsets[e], re = row_offsets[e + 1];
+    const int nk = (re - rs + kBK - 1) / kBK;
+    const __amdgpu_buffer_rsrc_t rA = make_rsrc(A + (int64_t)rs * Na, (uint32_t)(re - rs) * (uint32_t)Na * 2);
+    const __amdgpu_buffer_rsrc_t rB = make_rsrc(B + (int64_t)rs * Nb, (uint32_t)(re - rs) * (uint32_t)Nb * 2);
+    uint32_t oa[IA], ob[IB];
+#pragma unroll
+    for (int i = 0; i < IA; ++i) {
+      const int kr = wave * KR + i * RPI_A + lane / LPR_A;
+      const int lc = (lane % LPR_A) ^ kr_swz(kr);
+      int ca = a0 + lc * 8;
+      ca = ca < Na ? ca : Na - 8;
+      oa[i] = ((uint32_t)kr * (uint32_t)Na + (uint32_t)ca) * 2;
+    }
+#pragma unroll
+    for (int i = 0; i < IB; ++i) {
+      const int kr = wave * KR + i * RPI_B + lane / LPR_B;
+      const int lc = (lane % LPR_B) ^ kr_swz(kr);
+      int cb = b0 + lc * 8;
+      cb = cb < Nb ? cb : Nb - 8;
+      ob[i] = ((uint32_t)kr * (uint32_t)Nb + (uint32_t)cb) * 2;
+    }
+    auto issue = [&](int kt, int stage) __attribute__((always_inline)) {
+      char* sa = smem + stage * STAGE_BYTES;
+      char* sb = sa + TA_BYTES;
+      const uint32_t sofa = (uint32_t)kt * kBK * (uint32_t)Na * 2;
+      const uint32_t sofb = (uint32_t)kt * kBK * (uint32_t)Nb * 2;
+#pragma unroll
+      for (int i = 0; i < IA; ++i) dma16(rA, sa + (wave * KR + i * RPI_A) * (BA * 2), oa[i], sofa);
+#pragma unroll
+      for (int i = 0; i < IB; ++i) dma16(rB, sb + (wave * KR + i * RPI_B) * (BB * 2), ob[i], sofb);
+    };
+
+    floatx16 acc[NB][MB];
+#pragma unroll
+    for (int b = 0; b < NB; ++b)
+#pragma unroll
+      for (int a = 0; a < MB; ++a)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) acc[b][a][v] = 0.0f;
+
+#pragma unroll
+    for (int st = 0; st < STAGES - 1; ++st)
+      if (st < nk) issue(st, st);
+    for (int kt = 0; kt < nk; ++kt) {
+      wait_stages<PER, STAGES - 2>(min(STAGES - 2, nk - 1 - kt));
+      barrier_lds();
+      if (kt + STAGES - 1 < nk) issue(kt + STAGES - 1, (kt + STAGES - 1) % STAGES);
+      const char* la = smem + (kt % STAGES) * STAGE_BYTES;
+      const char* lb = la + TA_BYTES;
+      u32x4 fb[2][NB], fa[2][MB];
+      auto load_frags = [&](int sub, u32x4 (&xb)[NB], u32x4 (&xa)[MB]) __attribute__((always_inline)) {
+#pragma unroll
+        for (int b = 0; b < NB; ++b) xb[b] = tr_operand<BB>(lb, wn * (BB / WGN) + b * 32, sub, lane);
+#pragma unroll
+        for (int a = 0; a < MB; ++a) xa[a] = tr_operand<BA>(la, wm * (BA / 2) + a * 32, sub, lane);
+      };
+      load_frags(0, fb[0], fa[0]);
+#pragma unroll
+      for (int sub = 0; sub < kBK / 16; ++sub) {
+        if (sub + 1 < kBK / 16) load_frags(sub + 1, fb[(sub + 1) & 1], fa[(sub + 1) & 1]);
+#pragma unroll
+        for (int b = 0; b < NB; ++b)
+#pragma unroll
+          for (int a = 0; a < MB; ++a) acc[b][a] = TR::mfma32(fb[sub & 1][b], fa[sub & 1][a], acc[b][a]);
+      }
+    }
+
+    // Epilogue: no DMA is in flight (every issued step was consumed), so once
+    // all waves pass the barrier the whole ring is free for staging.
+    {
+      constexpr int WCOLS = BB / WGN;                     // output columns (nb) per wave
+      constexpr int PITCH = WCOLS * 2;
+      constexpr int C8 = PITCH / 8;
+      constexpr int RP = 256 / PITCH;
+      constexpr int REGION = STAGES * STAGE_BYTES / NW;
+      constexpr int FIT = REGION / (32 * PITCH);
+      constexpr int APP = FIT >= 4 && MB >= 4 ? 4 : (FIT >= 2 && MB >= 2 ? 2 : 1);
+      constexpr int LPR = PITCH / 16;
+      constexpr int RPI = 64 / LPR;
+      static_assert(FIT >= 1 && MB % APP == 0 && RP * C8 == 32, "staging layout");
+      const int rows = min(BA, Na - a0);
+      const __amdgpu_buffer_rsrc_t rC =
+          make_rsrc(C + ((int64_t)e * Na + a0) * Nb, (uint32_t)rows * (uint32_t)Nb * 2);
+      char* stg = smem + wave * REGION;
+      const int col0 = b0 + wn * WCOLS;
+      barrier_lds();
+#pragma unroll
+      for (int p0 = 0; p0 < MB; p0 += APP) {
+#pragma unroll
+        for (int a = p0; a < p0 + APP; ++a) {
+          const int r = (a - p0) * 32 + (lane & 31);
+          const int g = (r / RP) % C8;
+#pragma unroll
+          for (int b = 0; b < NB; ++b)
+#pragma unroll
+            for (int gq = 0; gq < 4; ++gq) {
+              const int ch8 = (b * 32 + gq * 8) / 4 + (lane >> 5);
+              *reinterpret_cast<u32x2*>(stg + r * PITCH + ((ch8 ^ g) << 3)) =
+                  pack4<TR>(acc[b][a][gq * 4 + 0], acc[b][a][gq * 4 + 1], acc[b][a][gq * 4 + 2], acc[b][a][gq * 4 + 3]);
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < APP * 32 / RPI; ++i) {
+          const int r = i * RPI + lane / LPR;
+          const int c16 = lane % LPR;
+          const int g = (r / RP) % C8;
+          u32x4 v = *reinterpret_cast<const u32x4*>(stg + r * PITCH + ((c16 ^ (g >> 1)) << 4));
+          if (g & 1) v = u32x4{v[2], v[3], v[0], v[1]};
+          const uint32_t ml = (uint32_t)(wm * (BA / 2) + p0 * 32 + r);
+          const int c = col0 + c16 * 8;
+          const uint32_t voff = c < Nb ? (ml * (uint32_t)Nb + (uint32_t)c) * 2 : 0x80000000u;
+          bstore16(rC, voff, v);
+        }
+      }
+    }
+  }
+  wait_vmcnt<0>();
+}
+
 // Wgrad fed by DMA: both operands are [64 rows][128 cols] tiles of the
 // expert's rows; rows past the expert's end read as zeros (buffer bounds).
 template <typename TR, int STAGES>
@@ -1238,7 +1403,19 @@ int launch_wgrad(const void* A, const void* B, const int64_t* tpe, int64_t M, in
                w.row_offsets, E, Na, Nb, w.work_counter);
     return HRM_MOE_OK;
   }
-  static const char* env = getenv("HRM_MOE_WGRAD_STAGES");
+  // 256 x 256 tiles with 8 waves when both widths fill them and experts have
+  // enough rows to amortise a tile; HRM_MOE_WGRAD_STAGES=2|3 selects the
+  // 128 x 128 four-wave kernel instead.
+  const char* env = getenv("HRM_MOE_WGRAD_STAGES");  // read per call: tests switch kernels in one process
+  if (env && !*env) env = nullptr;
+  if (!env && Na >= 256 && Nb >= 256 && M >= (int64_t)E * 256) {
+    auto kern = wgrad_dma8_kernel<TR, 256, 256, 8, 2>;
+    static int grid = 0;
+    if (grid == 0) grid = persistent_grid(kern, 512);
+    HRM_LAUNCH(kern, dim3(grid), dim3(512), 0, stream, (const uint16_t*)A, (const uint16_t*)B, (uint16_t*)C,
+               w.row_offsets, E, Na, Nb, w.work_counter);
+    return HRM_MOE_OK;
+  }
   const int stages = env && atoi(env) == 2 ? 2 : 3;
   if (stages == 2) {
     auto kern = wgrad_dma_kernel<TR, 2>;

@@ -1,5 +1,8 @@
 """Every built tile variant of the DMA grouped GEMMs gives the same bits.
 
+The wgrad kernels (8-wave 256 x 256 and the 4-wave 128 x 128 ones with 2 or 3
+stages, HRM_MOE_WGRAD_STAGES) are checked the same way.
+
 The variants differ in tile shape (128 x 128 with 4 waves, 256 x 256 with 8
 waves), pipeline depth and K step (64 or 32), and the gate/up kernel's
 256 x 256 variant runs its last N tile as a half tile when the width is an odd
@@ -76,3 +79,28 @@ def test_nt_nn_variants_identical(cuda, m, n, kk, e):
     _assert_same(_run_all(lambda: ops.grouped_gemm_nt(a, w, tpe)), f"nt {m}x{n}x{kk}")
     g = torch.from_numpy(synth.normal(83, (m, n))).to(cuda, torch.bfloat16)
     _assert_same(_run_all(lambda: ops.grouped_gemm_nn(g, w, tpe)), f"nn {m}x{kk}x{n}")
+
+
+def _run_wgrad(fn):
+    out = {}
+    old = os.environ.get("HRM_MOE_WGRAD_STAGES")
+    try:
+        for v in ["", "2", "3"]:
+            os.environ["HRM_MOE_WGRAD_STAGES"] = v
+            out[v or "default"] = fn()
+            torch.cuda.synchronize()
+    finally:
+        if old is None:
+            os.environ.pop("HRM_MOE_WGRAD_STAGES", None)
+        else:
+            os.environ["HRM_MOE_WGRAD_STAGES"] = old
+    return out
+
+
+@pytest.mark.parametrize("m,na,nb,e", [(4096, 512, 768, 8), (3000, 1024, 256, 4)])
+def test_wgrad_variants_identical(cuda, m, na, nb, e):
+    tpe = torch.from_numpy(_ragged(m + 7, m, e)).to(cuda)
+    g = torch.from_numpy(synth.normal(91, (m, na))).to(cuda, torch.bfloat16)
+    a = torch.from_numpy(synth.normal(92, (m, nb))).to(cuda, torch.bfloat16)
+    outs = _run_wgrad(lambda: ops.grouped_gemm_tn(g, a, tpe))
+    _assert_same(outs, f"tn {m}x{na}x{nb}")
