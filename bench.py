@@ -15,7 +15,8 @@ pass); the roofline of the dominant kernel (fused gate_up + SwiGLU GEMM, from
 those events on its stream) and the reference's eager CPU path timed on the
 host's cores over a bounded sample.
 
-Usage: python bench.py [--steps K] [--warmup W] [--gpus 1] [--workload l64x8|xl_skew|xl128|decode_t{1,8,64,256}]
+Usage: python bench.py [--steps K] [--warmup W] [--gpus 1]
+                       [--workload l64x8|xl_skew|xl128|decode_t{1,8,64,256}|xl128_train]
        python bench.py --calibrate-copy-mb 512   (a plain copy, for scaling rocprofv3 byte counters)
 """
 from __future__ import annotations
@@ -46,6 +47,8 @@ WORKLOADS = {
     "decode_t8": (8, 1536, 64, 512, 8, 0.0),
     "decode_t64": (64, 1536, 64, 512, 8, 0.0),
     "decode_t256": (256, 1536, 64, 512, 8, 0.0),
+    # XL 128x8 training GEMMs: forward, dgrad and wgrad of both grouped linears
+    "xl128_train": (32768, 1536, 128, 512, 8, 0.0),
 }
 
 
@@ -250,6 +253,60 @@ def run_decode(args, hrm, dev):
     print(json.dumps(result), flush=True)
 
 
+def run_train_gemms(args, hrm, dev):
+    """XL 128x8 grouped linears, forward + backward (dgrad and wgrad) through hip_grouped_linear's autograd.
+
+    One step: gate_up = A[R,H] . W_gu[e]^T and down = act[R,I] . W_dn[e]^T
+    forward, then backward with N(0,1) upstream grads.  Rows are split evenly
+    over the experts (the near-uniform routing of N(0,0.02) gates).  Work per
+    step: 3 x 2 x R x (H x 2I + I x H) flops.
+    """
+    t, h, e, i, k, _ = WORKLOADS[args.workload]
+    r = t * k
+    g = torch.Generator(device=dev).manual_seed(7)
+    bf = torch.bfloat16
+    tpe = torch.full((e,), r // e, dtype=torch.int64, device=dev)
+    tpe[: r - int(tpe.sum())] += 1
+    a = torch.randn(r, h, device=dev, generator=g).to(bf).requires_grad_(True)
+    act = torch.randn(r, i, device=dev, generator=g).to(bf).requires_grad_(True)
+    w_gu = (torch.randn(e, 2 * i, h, device=dev, generator=g) * 0.02).to(bf).requires_grad_(True)
+    w_dn = (torch.randn(e, h, i, device=dev, generator=g) * 0.02).to(bf).requires_grad_(True)
+    d_gu = torch.randn(r, 2 * i, device=dev, generator=g).to(bf)
+    d_dn = torch.randn(r, h, device=dev, generator=g).to(bf)
+
+    def step():
+        y1 = hrm.hip_grouped_linear(a, w_gu, tpe)
+        y2 = hrm.hip_grouped_linear(act, w_dn, tpe)
+        torch.autograd.backward([y1, y2], [d_gu, d_dn])
+        a.grad = act.grad = w_gu.grad = w_dn.grad = None
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(args.steps):
+        step()
+    end.record()
+    torch.cuda.synchronize()
+    ms = start.elapsed_time(end) / args.steps
+    flops = 3 * 2.0 * r * (h * 2 * i + i * h)
+    tflops = flops / (ms * 1e-3) / 1e12
+    log(f"xl128 training GEMMs: {ms:.4f} ms per step, {tflops:.1f} TFLOP/s")
+    print(json.dumps({
+        "metric": "XL 128x8 grouped GEMMs forward + dgrad + wgrad, TFLOP/s (% bf16 MFMA peak)",
+        "value": round(tflops, 2), "unit": "TFLOP/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(ms, 5), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "bf16", "data": "synthetic",
+        "config": {"workload": f"xl128_train: gate_up and down grouped linears of {r} rows, H={h}, E={e}, I={i}, "
+                               f"forward + backward with N(0,1) upstream grads", "rows": r, "hidden": h,
+                   "experts": e, "inter": i},
+        "pct_bf16_peak": round(100 * tflops / PEAK_BF16_TFLOPS, 2),
+        "flops_per_step": flops,
+    }), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -274,6 +331,9 @@ def main():
     dev = torch.device("cuda:0")
     if args.workload.startswith("decode"):
         run_decode(args, hrm, dev)
+        return
+    if args.workload == "xl128_train":
+        run_train_gemms(args, hrm, dev)
         return
     t, h, e, i, k, bias = WORKLOADS[args.workload]
     r = t * k
