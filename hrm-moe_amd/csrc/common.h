@@ -30,6 +30,9 @@ struct BF16 {
   static __device__ __forceinline__ floatx16 mfma32(u32x4 a, u32x4 b, floatx16 c) {
     return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
   }
+  static __device__ __forceinline__ floatx4 mfma16(u32x4 a, u32x4 b, floatx4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+  }
 };
 
 struct F16 {
@@ -37,6 +40,9 @@ struct F16 {
   static __device__ __forceinline__ uint16_t from_f(float f) { return __builtin_bit_cast(uint16_t, static_cast<_Float16>(f)); }
   static __device__ __forceinline__ floatx16 mfma32(u32x4 a, u32x4 b, floatx16 c) {
     return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(halfx8, a), __builtin_bit_cast(halfx8, b), c, 0, 0, 0);
+  }
+  static __device__ __forceinline__ floatx4 mfma16(u32x4 a, u32x4 b, floatx4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(halfx8, a), __builtin_bit_cast(halfx8, b), c, 0, 0, 0);
   }
 };
 

@@ -959,6 +959,123 @@ __global__ __launch_bounds__(NW * 64, NW == 4 ? 2 : 1) void mgemm_dma_kernel(con
   wait_vmcnt<0>();
 }
 
+// Skinny M-grouped GEMM for decode-sized inputs (a few rows per expert).
+// Workgroup (e, cb) computes output columns [16 cb, 16 cb + 16) for every row
+// of expert e with v_mfma_f32_16x16x32: the 16 weight rows are the MFMA A
+// operand and up to 16 rows of the expert the B operand, both loaded from
+// global memory straight into the operand layout (lane l: row l % 16,
+// k = 8 (l / 16) .. +7, 16 contiguous bytes), so the kernel streams each
+// weight row once with no LDS staging.  The 4 waves split K; each keeps PD
+// 32-wide K chunks of loads in flight (a register ring) and the 4 partial
+// sums are added in LDS in wave order.  Rows come in passes of 16 NRB; the
+// weights are re-read per pass, which only matters for experts far above the
+// decode sizes this kernel is chosen for.
+template <typename TR, int KIND, int NRB>
+__global__ __launch_bounds__(256) void mgemm_skinny_kernel(const uint16_t* __restrict__ A,
+                                                           const int32_t* __restrict__ gather,
+                                                           const uint16_t* __restrict__ W, uint16_t* __restrict__ C,
+                                                           const int64_t* __restrict__ tpe, int E, int M, int N, int K,
+                                                           int cblk_n) {
+  static_assert(KIND == KIND_NT || KIND == KIND_GATHER_SWIGLU, "skinny kernel: NT or gate/up");
+  constexpr bool SW = KIND == KIND_GATHER_SWIGLU;
+  constexpr int PD = 4;  // K chunks in flight per wave
+  __shared__ floatx4 red[4][NRB][SW ? 2 : 1][64];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int e = blockIdx.x / cblk_n;
+  const int c0 = (blockIdx.x - e * cblk_n) * 16;
+
+  // rows of expert e: prefix of tokens_per_expert, clamped to M
+  int64_t before = 0;
+  for (int c = 0; c < e; c += 64) {
+    const int ee = c + lane;
+    int64_t v = ee < e ? tpe[ee] : 0;
+    v = v > 0 ? v : 0;
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    before += v;
+  }
+  int64_t cnt = tpe[e];
+  cnt = cnt > 0 ? cnt : 0;
+  const int rs = (int)(before < M ? before : M);
+  const int re = (int)(before + cnt < M ? before + cnt : M);
+  if (re <= rs) return;  // uniform over the workgroup
+
+  const int w_rows = SW ? 2 * N : N;
+  const uint16_t* wg = W + ((int64_t)e * w_rows + c0 + (lane & 15)) * K + (lane >> 4) * 8;
+  const uint16_t* wu = SW ? wg + (int64_t)N * K : wg;
+  const int nc = K / 32;
+  const int kc0 = wave * nc / 4, kc1 = (wave + 1) * nc / 4;
+
+  for (int p = rs; p < re; p += 16 * NRB) {
+    const uint16_t* xr[NRB];
+#pragma unroll
+    for (int rb = 0; rb < NRB; ++rb) {
+      int r = p + rb * 16 + (lane & 15);
+      r = r < re ? r : re - 1;  // rows past the expert repeat a valid one; their columns are never stored
+      const int64_t src = SW ? (int64_t)gather[r] : (int64_t)r;
+      xr[rb] = A + src * K + (lane >> 4) * 8;
+    }
+    floatx4 ag[NRB], au[NRB];
+#pragma unroll
+    for (int rb = 0; rb < NRB; ++rb) {
+      ag[rb] = floatx4{0.f, 0.f, 0.f, 0.f};
+      au[rb] = floatx4{0.f, 0.f, 0.f, 0.f};
+    }
+    if (kc1 > kc0) {
+      u32x4 bg[PD], bu[PD], bx[PD][NRB];
+      // loads of chunk kc into ring slot u; chunks past the wave's range reload its last one
+      auto load = [&](int u, int kc) __attribute__((always_inline)) {
+        const int k = (kc < kc1 ? kc : kc1 - 1) * 32;
+        bg[u] = ld16(wg + k);
+        if constexpr (SW) bu[u] = ld16(wu + k);
+#pragma unroll
+        for (int rb = 0; rb < NRB; ++rb) bx[u][rb] = ld16(xr[rb] + k);
+      };
+#pragma unroll
+      for (int u = 0; u < PD; ++u) load(u, kc0 + u);
+      for (int kc = kc0; kc < kc1; kc += PD) {
+#pragma unroll
+        for (int u = 0; u < PD; ++u) {
+          if (kc + u < kc1) {
+#pragma unroll
+            for (int rb = 0; rb < NRB; ++rb) {
+              ag[rb] = TR::mfma16(bg[u], bx[u][rb], ag[rb]);
+              if constexpr (SW) au[rb] = TR::mfma16(bu[u], bx[u][rb], au[rb]);
+            }
+            load(u, kc + u + PD);
+          }
+        }
+      }
+    }
+#pragma unroll
+    for (int rb = 0; rb < NRB; ++rb) {
+      red[wave][rb][0][lane] = ag[rb];
+      if constexpr (SW) red[wave][rb][1][lane] = au[rb];
+    }
+    __syncthreads();
+    // waves 0..NRB-1 reduce one column block each: the 4 K quarters in wave order
+    if (wave < NRB) {
+      const int rb = wave;
+      floatx4 g = red[0][rb][0][lane], u = floatx4{0.f, 0.f, 0.f, 0.f};
+      if constexpr (SW) u = red[0][rb][1][lane];
+#pragma unroll
+      for (int w = 1; w < 4; ++w) {
+        g += red[w][rb][0][lane];
+        if constexpr (SW) u += red[w][rb][1][lane];
+      }
+      const int r = p + rb * 16 + (lane & 15);  // D: lane l holds rows c0 + 4 (l/16) + v of column l % 16
+      if (r < re) {
+        float o[4];
+#pragma unroll
+        for (int v = 0; v < 4; ++v) o[v] = SW ? swiglu_fast<TR>(g[v], u[v]) : g[v];
+        st8(C + (int64_t)r * N + c0 + (lane >> 4) * 4, pack4<TR>(o[0], o[1], o[2], o[3]));
+      }
+    }
+    __syncthreads();  // red[] is reused by the next pass
+  }
+}
+
 // Wgrad with 8 waves on BA x BB = 256 x 256 tiles of C[e] (128 x 64 per
 // wave), both operands DMA-fed as [64 k][cols] slices of the expert's rows
 // and read transposed.  Tiles are handed out by one atomic counter per XCD
@@ -1354,6 +1471,29 @@ int dispatch_mgemm_t(const void* A, const int32_t* gather, const void* W, const 
                                  : launch_mgemm<TR, KIND, 128, 128>(A, gather, W, tpe, M, N, K, E, C, workspace, stream);
   }
   // weight rows spanned by the N tiles: 2N for the gate/up pair, else N
+  // Decode sizes: at most one row per four experts on average (a token or two
+  // at top-8 of 64) -> weight-streaming skinny kernel.  Measured against the
+  // tiled kernels it wins only there (T = 1: gate_up 17 vs 26 us); from about
+  // one row per expert the tiled DMA kernels stream weights faster.
+  // HRM_MOE_SKINNY=1 forces it up to 16 rows per expert, =0 turns it off
+  // (tests compare both paths).
+  if constexpr (KIND != KIND_NN) {
+    const char* sk = getenv("HRM_MOE_SKINNY");
+    const bool force = sk && sk[0] == '1', off = sk && sk[0] == '0';
+    const int64_t limit = force ? (int64_t)E * 16 : (int64_t)E / 4;
+    const bool skinny_ok = !off && M <= limit && K % 32 == 0 && N % 16 == 0;
+    if (skinny_ok) {
+      const int cblk_n = N / 16;
+      const dim3 grid((unsigned)(E * cblk_n));
+      if (M <= (int64_t)E * 4)  // up to 4 rows per expert on average: one 16-row block per pass
+        HRM_LAUNCH((mgemm_skinny_kernel<TR, KIND, 1>), grid, dim3(256), 0, stream, (const uint16_t*)A, gather,
+                   (const uint16_t*)W, (uint16_t*)C, tpe, E, (int)M, N, K, cblk_n);
+      else
+        HRM_LAUNCH((mgemm_skinny_kernel<TR, KIND, 2>), grid, dim3(256), 0, stream, (const uint16_t*)A, gather,
+                   (const uint16_t*)W, (uint16_t*)C, tpe, E, (int)M, N, K, cblk_n);
+      return HRM_MOE_OK;
+    }
+  }
   MCfg c = mgemm_cfg(M, E, KIND == KIND_GATHER_SWIGLU ? 2 * (int64_t)N : (int64_t)N, KIND == KIND_GATHER_SWIGLU);
   if (K % c.bk != 0) c = MCfg{128, 128, 2, 4, 64};
   // the ring may run at most one tile ahead: STAGES - 1 <= K / BK
