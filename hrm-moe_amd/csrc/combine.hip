@@ -3,10 +3,10 @@
 // Replaces models/layers.py:333-334 of the reference:
 //   expert_output = expert_output * sorted_weights[:, None]
 //   final_hidden_states.index_add_(0, sorted_token_idx, expert_output)
-// as a gather instead of a scatter: one wavefront per token reads the token's
-// k rows (slot_to_row), multiplies each by its routing weight with a rounding
-// to the element type (the reference multiplies 16-bit tensors), and adds the
-// products in fp32 in ascending row order, rounding once at the end.  That is
+// as a gather instead of a scatter.  Each token's k rows (slot_to_row) are
+// read and each is multiplied by its routing weight with a rounding to the
+// element type (the reference multiplies 16-bit tensors); the products are
+// added in fp32 in ascending row order and rounded once at the end.  That is
 // the arithmetic of the reference's index_add_ on the CPU.  The gather does
 // no atomics, so the result is the same on every run.
 #include "common.h"
@@ -24,6 +24,7 @@ struct Elem<HRM_MOE_BF16> {
     return BF16::to_f((uint16_t)((q & 1) ? (w >> 16) : (w & 0xffff)));
   }
   static __device__ __forceinline__ float round(float f) { return BF16::to_f(BF16::from_f(f)); }
+  static __device__ __forceinline__ float mul(float a, float b) { return round(a * b); }
   static __device__ __forceinline__ float weight(const void* p, int64_t i) { return BF16::to_f(reinterpret_cast<const uint16_t*>(p)[i]); }
   static __device__ __forceinline__ u32x4 pack(const float* a) {
     return u32x4{pack2(BF16::from_f(a[0]), BF16::from_f(a[1])), pack2(BF16::from_f(a[2]), BF16::from_f(a[3])),
@@ -38,6 +39,7 @@ struct Elem<HRM_MOE_F16> {
     return F16::to_f((uint16_t)((q & 1) ? (w >> 16) : (w & 0xffff)));
   }
   static __device__ __forceinline__ float round(float f) { return F16::to_f(F16::from_f(f)); }
+  static __device__ __forceinline__ float mul(float a, float b) { return round(a * b); }
   static __device__ __forceinline__ float weight(const void* p, int64_t i) { return F16::to_f(reinterpret_cast<const uint16_t*>(p)[i]); }
   static __device__ __forceinline__ u32x4 pack(const float* a) {
     return u32x4{pack2(F16::from_f(a[0]), F16::from_f(a[1])), pack2(F16::from_f(a[2]), F16::from_f(a[3])),
@@ -50,91 +52,97 @@ struct Elem<HRM_MOE_F32> {
   static __device__ __forceinline__ float get(const u32x4& v, int q) { return __uint_as_float(v[q]); }
   static __device__ __forceinline__ float round(float f) { return f; }
   static __device__ __forceinline__ float weight(const void* p, int64_t i) { return reinterpret_cast<const float*>(p)[i]; }
+  // the product is rounded before the add, as the reference's separate
+  // multiply is: device code contracts a * b + c into an FMA by default
+  static __device__ __forceinline__ float mul(float a, float b) {
+#pragma clang fp contract(off)
+    return a * b;
+  }
   static __device__ __forceinline__ u32x4 pack(const float* a) {
     return u32x4{__float_as_uint(a[0]), __float_as_uint(a[1]), __float_as_uint(a[2]), __float_as_uint(a[3])};
   }
 };
 
-constexpr int kWavesPerBlock = 4;
-constexpr int kMaxTopK = 32;
+constexpr int kTokPerBlock = 8;
+constexpr int kBlock = 256;
+constexpr int kMaxTopK = 32;  // kTokPerBlock * kMaxTopK <= kBlock: one thread per routed slot
 
-// KU > 0: top-k fixed at compile time, so every row load of a chunk is issued
+// A block combines kTokPerBlock consecutive tokens.  Its threads first rank
+// each token's k rows (ascending row order is the summation order) into LDS,
+// then stride over (token, 16-byte chunk) items, so no lane idles when a
+// token's chunk count is not a multiple of the wave size.
+// KU > 0: top-k fixed at compile time, so every row load of an item is issued
 // before the first product is added (all k loads in flight per lane).
 // KU == 0: any top-k up to kMaxTopK, rows loaded one after another.
 template <int DT, int KU>
-__global__ __launch_bounds__(kWavesPerBlock * 64) void combine_kernel(const char* __restrict__ Y,
-                                                                     const int32_t* __restrict__ slot_to_row,
-                                                                     const void* __restrict__ wts,
-                                                                     const int32_t* __restrict__ expert_offsets,
-                                                                     int64_t T, int k, int64_t H, int E,
-                                                                     char* __restrict__ out) {
+__global__ __launch_bounds__(kBlock) void combine_kernel(const char* __restrict__ Y,
+                                                        const int32_t* __restrict__ slot_to_row,
+                                                        const void* __restrict__ wts,
+                                                        const int32_t* __restrict__ expert_offsets, int64_t T,
+                                                        int k, int64_t H, int E, char* __restrict__ out) {
   using El = Elem<DT>;
   constexpr int P = El::kPer16;
   constexpr int ESZ = 16 / P;
-  __shared__ int32_t s_row[kWavesPerBlock][kMaxTopK];
-  __shared__ float s_w[kWavesPerBlock][kMaxTopK];
-  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
-  const int64_t t = (int64_t)blockIdx.x * kWavesPerBlock + wv;
-  const bool active = t < T;  // every wave reaches the barrier
+  __shared__ int32_t s_raw[kTokPerBlock * kMaxTopK];
+  __shared__ int32_t s_row[kTokPerBlock][kMaxTopK];
+  __shared__ float s_w[kTokPerBlock][kMaxTopK];
+  const int tid = threadIdx.x;
+  const int64_t t0 = (int64_t)blockIdx.x * kTokPerBlock;
+  const int ntok = (int)(T - t0 < kTokPerBlock ? T - t0 : kTokPerBlock);
+  const int nslot = ntok * k;
   const int32_t r_valid = expert_offsets[E];
-  int32_t row = 0x7fffffff;
+  int32_t row = 0;
   float w = 0.0f;
-  if (active && lane < k) {
-    row = slot_to_row[t * k + lane];
-    w = El::weight(wts, t * k + lane);
-  }
-  // Rank of this lane's row among the token's k rows (rows are distinct).
-  int rank = 0;
-  for (int j = 0; j < k; ++j) {
-    const int32_t other = __shfl(row, j);
-    rank += (other < row) ? 1 : 0;
-  }
-  if (active && lane < k) {
-    s_row[wv][rank] = row;
-    s_w[wv][rank] = w;
+  if (tid < nslot) {
+    row = slot_to_row[t0 * k + tid];
+    w = El::weight(wts, t0 * k + tid);
+    s_raw[tid] = row;
   }
   __syncthreads();
-  if (!active) return;
-  const int64_t chunks = H / P;
-  if constexpr (KU > 0) {
-    int64_t roff[KU];
-    float wj[KU];
-    bool ok[KU];
+  // Rank of this slot's row among its token's k rows (rows are distinct).
+  if (tid < nslot) {
+    const int tk = tid / k;
+    const int32_t* rows = s_raw + tk * k;
+    int rank = 0;
+    for (int j = 0; j < k; ++j) rank += rows[j] < row ? 1 : 0;
+    s_row[tk][rank] = row;
+    s_w[tk][rank] = w;
+  }
+  __syncthreads();
+  const int chunks = (int)(H / P);
+  const int items = ntok * chunks;
+  for (int it = tid; it < items; it += kBlock) {
+    const int tk = it / chunks;
+    const int c = it - tk * chunks;
+    float acc[P];
 #pragma unroll
-    for (int j = 0; j < KU; ++j) {
-      const int32_t r = s_row[wv][j];
-      ok[j] = r < r_valid;  // dropped rows hold no expert output
-      roff[j] = (int64_t)(ok[j] ? r : 0) * H;
-      wj[j] = s_w[wv][j];
-    }
-    for (int64_t c = lane; c < chunks; c += 64) {
+    for (int q = 0; q < P; ++q) acc[q] = 0.0f;
+    if constexpr (KU > 0) {
       u32x4 y[KU];
+      bool ok[KU];
 #pragma unroll
-      for (int j = 0; j < KU; ++j) y[j] = ld16(Y + (roff[j] + c * P) * ESZ);
-      float acc[P];
-#pragma unroll
-      for (int q = 0; q < P; ++q) acc[q] = 0.0f;
-#pragma unroll
-      for (int j = 0; j < KU; ++j)
-#pragma unroll
-        for (int q = 0; q < P; ++q) acc[q] = ok[j] ? acc[q] + El::round(El::get(y[j], q) * wj[j]) : acc[q];
-      st16(out + (t * H + c * P) * ESZ, El::pack(acc));
-    }
-  } else {
-    for (int64_t c = lane; c < chunks; c += 64) {
-      float acc[P];
-#pragma unroll
-      for (int q = 0; q < P; ++q) acc[q] = 0.0f;
-      for (int j = 0; j < k; ++j) {
-        const int32_t r = s_row[wv][j];
-        if (r >= r_valid) continue;
-        const float wj = s_w[wv][j];
-        const u32x4 y = ld16(Y + ((int64_t)r * H + c * P) * ESZ);
-#pragma unroll
-        for (int q = 0; q < P; ++q) acc[q] += El::round(El::get(y, q) * wj);
+      for (int j = 0; j < KU; ++j) {
+        const int32_t r = s_row[tk][j];
+        ok[j] = r < r_valid;  // dropped rows hold no expert output
+        y[j] = ld16(Y + ((int64_t)(ok[j] ? r : 0) * H + (int64_t)c * P) * ESZ);
       }
-      st16(out + (t * H + c * P) * ESZ, El::pack(acc));
+#pragma unroll
+      for (int j = 0; j < KU; ++j) {
+        const float wj = s_w[tk][j];
+#pragma unroll
+        for (int q = 0; q < P; ++q) acc[q] = ok[j] ? acc[q] + El::mul(El::get(y[j], q), wj) : acc[q];
+      }
+    } else {
+      for (int j = 0; j < k; ++j) {
+        const int32_t r = s_row[tk][j];
+        if (r >= r_valid) continue;
+        const float wj = s_w[tk][j];
+        const u32x4 y = ld16(Y + ((int64_t)r * H + (int64_t)c * P) * ESZ);
+#pragma unroll
+        for (int q = 0; q < P; ++q) acc[q] += El::mul(El::get(y, q), wj);
+      }
     }
+    st16(out + ((t0 + tk) * H + (int64_t)c * P) * ESZ, El::pack(acc));
   }
 }
 
@@ -166,7 +174,8 @@ extern "C" int hrm_moe_combine(const void* expert_out, const int32_t* slot_to_ro
   if (top_k > hrm::kMaxTopK || hidden_size % 8) return HRM_MOE_ERR_UNSUPPORTED;
   if (num_tokens == 0) return HRM_MOE_OK;
   if (!expert_out || !slot_to_row || !topk_weight || !expert_offsets || !out) return HRM_MOE_ERR_INVALID;
-  dim3 grid((unsigned)((num_tokens + hrm::kWavesPerBlock - 1) / hrm::kWavesPerBlock)), block(hrm::kWavesPerBlock * 64);
+  if (hidden_size / 8 > (int64_t(1) << 27)) return HRM_MOE_ERR_UNSUPPORTED;  // items per block fit an int
+  dim3 grid((unsigned)((num_tokens + hrm::kTokPerBlock - 1) / hrm::kTokPerBlock)), block(hrm::kBlock);
   const char* Y = static_cast<const char*>(expert_out);
   char* O = static_cast<char*>(out);
   if (dtype == HRM_MOE_BF16)
