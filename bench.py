@@ -16,7 +16,7 @@ those events on its stream) and the reference's eager CPU path timed on the
 host's cores over a bounded sample.
 
 Usage: python bench.py [--steps K] [--warmup W] [--gpus 1]
-                       [--workload l64x8|xl_skew|xl128|decode_t{1,8,64,256}|xl128_train]
+                       [--workload l64x8|xl_skew|xl128|decode_t{1,8,64,256}|xl128_train|l64x8_train|xl_skew_train]
        python bench.py --calibrate-copy-mb 512   (a plain copy, for scaling rocprofv3 byte counters)
 """
 from __future__ import annotations
@@ -49,6 +49,9 @@ WORKLOADS = {
     "decode_t256": (256, 1536, 64, 512, 8, 0.0),
     # XL 128x8 training GEMMs: forward, dgrad and wgrad of both grouped linears
     "xl128_train": (32768, 1536, 128, 512, 8, 0.0),
+    # whole-layer training steps (forward + backward) at the L and XL-skew shapes
+    "l64x8_train": (16384, 1280, 64, 448, 8, 0.0),
+    "xl_skew_train": (16384, 1536, 64, 512, 8, 1.5),
 }
 
 
@@ -307,6 +310,72 @@ def run_train_gemms(args, hrm, dev):
     }), flush=True)
 
 
+def run_layer_train(args, hrm, dev):
+    """One training step of the whole MoE FFN layer: forward with the aux-loss context, then backward.
+
+    Upstream gradient g ~ N(0,1) on the output, plus the aux loss.  Gradients reach
+    the hidden states, the router weight and both expert weights.  Work per
+    step counted: the expert GEMMs, 6*R*H*I forward + 12*R*H*I backward (dgrad
+    and wgrad of both projections).  The same steps are also timed with the
+    reference's composition under autograd (fused_backward = False: torch ops
+    for gather, SwiGLU, weighting and index_add_, HIP grouped GEMMs).
+    """
+    t, h, e, i, k, bias = WORKLOADS[args.workload]
+    r = t * k
+    layers, xs = [], []
+    for c in range(args.weight_copies):
+        layer, x = make_layer(hrm, dev, t, h, e, i, k, bias, seed=1234 + c)
+        layers.append(layer)
+        xs.append(x.requires_grad_(True))
+    g = torch.randn(t, h, device=dev, generator=torch.Generator(device=dev).manual_seed(99)).to(torch.bfloat16)
+
+    def step(j):
+        layer = layers[j % len(layers)]
+        ctx = {}
+        out = layer(xs[j % len(xs)], moe_context=ctx)
+        torch.autograd.backward([out, torch.stack(ctx["aux_losses"]).sum()], [g, None])
+        for p in layer.parameters():
+            p.grad = None
+        xs[j % len(xs)].grad = None
+
+    def timed():
+        for j in range(args.warmup):
+            step(j)
+        torch.cuda.synchronize()
+        start = torch.cuda.Event(enable_timing=True)
+        end = torch.cuda.Event(enable_timing=True)
+        start.record()
+        for j in range(args.steps):
+            step(j)
+        end.record()
+        torch.cuda.synchronize()
+        return start.elapsed_time(end) / args.steps
+
+    ms = timed()
+    cls = type(layers[0].experts)
+    cls.fused_backward = False
+    try:
+        ms_ref = timed()
+    finally:
+        cls.fused_backward = True
+    flops = 18.0 * r * h * i
+    tflops = flops / (ms * 1e-3) / 1e12
+    log(f"{args.workload}: {ms:.4f} ms per training step ({tflops:.1f} TFLOP/s); "
+        f"reference composition under autograd {ms_ref:.4f} ms")
+    print(json.dumps({
+        "metric": f"MoE FFN layer training step (forward + backward), H={h}, E={e}, I={i}, top-{k}, {t} tokens",
+        "value": round(tflops, 2), "unit": "TFLOP/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(ms, 5), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "bf16", "data": "synthetic",
+        "config": {"workload": f"{args.workload}: MoE FFN layer forward + backward, N(0,1) output grads + aux loss, "
+                               f"{t} tokens, H={h}, E={e}, I={i}, top-{k}", "tokens": t, "hidden": h, "experts": e,
+                   "inter": i, "top_k": k, "weight_copies": args.weight_copies},
+        "pct_bf16_peak": round(100 * tflops / PEAK_BF16_TFLOPS, 2),
+        "flops_per_step": flops,
+        "reference_composition_ms_per_step": round(ms_ref, 5),
+    }), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -334,6 +403,9 @@ def main():
         return
     if args.workload == "xl128_train":
         run_train_gemms(args, hrm, dev)
+        return
+    if args.workload.endswith("_train"):
+        run_layer_train(args, hrm, dev)
         return
     t, h, e, i, k, bias = WORKLOADS[args.workload]
     r = t * k

@@ -26,6 +26,7 @@ struct Elem<HRM_MOE_BF16> {
   static __device__ __forceinline__ float round(float f) { return BF16::to_f(BF16::from_f(f)); }
   static __device__ __forceinline__ float mul(float a, float b) { return round(a * b); }
   static __device__ __forceinline__ float weight(const void* p, int64_t i) { return BF16::to_f(reinterpret_cast<const uint16_t*>(p)[i]); }
+  static __device__ __forceinline__ void store1(void* p, int64_t i, float v) { reinterpret_cast<uint16_t*>(p)[i] = BF16::from_f(v); }
   static __device__ __forceinline__ u32x4 pack(const float* a) {
     return u32x4{pack2(BF16::from_f(a[0]), BF16::from_f(a[1])), pack2(BF16::from_f(a[2]), BF16::from_f(a[3])),
                  pack2(BF16::from_f(a[4]), BF16::from_f(a[5])), pack2(BF16::from_f(a[6]), BF16::from_f(a[7]))};
@@ -41,6 +42,7 @@ struct Elem<HRM_MOE_F16> {
   static __device__ __forceinline__ float round(float f) { return F16::to_f(F16::from_f(f)); }
   static __device__ __forceinline__ float mul(float a, float b) { return round(a * b); }
   static __device__ __forceinline__ float weight(const void* p, int64_t i) { return F16::to_f(reinterpret_cast<const uint16_t*>(p)[i]); }
+  static __device__ __forceinline__ void store1(void* p, int64_t i, float v) { reinterpret_cast<uint16_t*>(p)[i] = F16::from_f(v); }
   static __device__ __forceinline__ u32x4 pack(const float* a) {
     return u32x4{pack2(F16::from_f(a[0]), F16::from_f(a[1])), pack2(F16::from_f(a[2]), F16::from_f(a[3])),
                  pack2(F16::from_f(a[4]), F16::from_f(a[5])), pack2(F16::from_f(a[6]), F16::from_f(a[7]))};
@@ -58,6 +60,7 @@ struct Elem<HRM_MOE_F32> {
 #pragma clang fp contract(off)
     return a * b;
   }
+  static __device__ __forceinline__ void store1(void* p, int64_t i, float v) { reinterpret_cast<float*>(p)[i] = v; }
   static __device__ __forceinline__ u32x4 pack(const float* a) {
     return u32x4{__float_as_uint(a[0]), __float_as_uint(a[1]), __float_as_uint(a[2]), __float_as_uint(a[3])};
   }
@@ -146,6 +149,120 @@ __global__ __launch_bounds__(kBlock) void combine_kernel(const char* __restrict_
   }
 }
 
+// Backward of the weighted combine, as torch autograd differentiates
+// models/layers.py:333-334 (expert_output * sorted_weights[:, None], then
+// index_add_):
+//   d_rows[row(t,j)] = round(dout[t] * w[t,j])
+//   d_w[t,j]         = round(sum_h round(dout[t,h] * rows[row(t,j),h]))
+// One wave per token, lanes striding over 16-byte chunks.  The per-slot sums
+// are reduced over the wave by a fixed xor butterfly, so every run gives the
+// same bits.  Slots whose row is a dropped one (>= expert_offsets[E]) get
+// d_w = 0 and no d_rows write.
+// KU > 0: top-k fixed at compile time, all slots handled per chunk.
+// KU == 0: any top-k, one slot at a time.
+constexpr int kBwdWaves = 4;
+template <int DT, int KU>
+__global__ __launch_bounds__(kBwdWaves * 64) void combine_bwd_kernel(const char* __restrict__ dout,
+                                                                    const char* __restrict__ Y,
+                                                                    const int32_t* __restrict__ slot_to_row,
+                                                                    const void* __restrict__ wts,
+                                                                    const int32_t* __restrict__ expert_offsets,
+                                                                    int64_t T, int k, int64_t H, int E,
+                                                                    char* __restrict__ dY, void* __restrict__ dW) {
+  using El = Elem<DT>;
+  constexpr int P = El::kPer16;
+  constexpr int ESZ = 16 / P;
+  const int lane = threadIdx.x & 63;
+  const int64_t t = (int64_t)blockIdx.x * kBwdWaves + (threadIdx.x >> 6);
+  if (t >= T) return;  // no barriers below
+  const int32_t r_valid = expert_offsets[E];
+  int32_t my_row = 0;
+  float my_w = 0.0f;
+  if (lane < k) {
+    my_row = slot_to_row[t * k + lane];
+    my_w = El::weight(wts, t * k + lane);
+  }
+  const int chunks = (int)(H / P);
+  const char* drow = dout + t * H * ESZ;
+  auto reduce = [](float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    return v;
+  };
+  if constexpr (KU > 0) {
+    int32_t row[KU];
+    float wj[KU], part[KU];
+    bool ok[KU];
+#pragma unroll
+    for (int j = 0; j < KU; ++j) {
+      row[j] = __shfl(my_row, j, 64);
+      wj[j] = __shfl(my_w, j, 64);
+      ok[j] = row[j] < r_valid;
+      part[j] = 0.0f;
+    }
+    for (int c = lane; c < chunks; c += 64) {
+      const u32x4 g = ld16(drow + (int64_t)c * 16);
+      u32x4 y[KU];
+#pragma unroll
+      for (int j = 0; j < KU; ++j) y[j] = ld16(Y + ((int64_t)(ok[j] ? row[j] : 0) * H + (int64_t)c * P) * ESZ);
+#pragma unroll
+      for (int j = 0; j < KU; ++j) {
+        float dy[P];
+#pragma unroll
+        for (int q = 0; q < P; ++q) {
+          const float gq = El::get(g, q);
+          part[j] += El::mul(gq, El::get(y[j], q));
+          dy[q] = El::mul(gq, wj[j]);
+        }
+        if (ok[j]) st16(dY + ((int64_t)row[j] * H + (int64_t)c * P) * ESZ, El::pack(dy));
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < KU; ++j) {
+      const float sj = reduce(part[j]);
+      if (lane == 0) El::store1(dW, t * k + j, ok[j] ? sj : 0.0f);
+    }
+  } else {
+    for (int j = 0; j < k; ++j) {
+      const int32_t r = __shfl(my_row, j, 64);
+      const float wj = __shfl(my_w, j, 64);
+      const bool ok = r < r_valid;
+      float part = 0.0f;
+      if (ok) {
+        for (int c = lane; c < chunks; c += 64) {
+          const u32x4 g = ld16(drow + (int64_t)c * 16);
+          const u32x4 y = ld16(Y + ((int64_t)r * H + (int64_t)c * P) * ESZ);
+          float dy[P];
+#pragma unroll
+          for (int q = 0; q < P; ++q) {
+            const float gq = El::get(g, q);
+            part += El::mul(gq, El::get(y, q));
+            dy[q] = El::mul(gq, wj);
+          }
+          st16(dY + ((int64_t)r * H + (int64_t)c * P) * ESZ, El::pack(dy));
+        }
+      }
+      const float sj = reduce(part);  // every lane takes part: the shuffles need the whole wave
+      if (lane == 0) El::store1(dW, t * k + j, ok ? sj : 0.0f);
+    }
+  }
+}
+
+template <int DT>
+void launch_combine_bwd(void* stream, const char* dout, const char* Y, const int32_t* slot_to_row, const void* wts,
+                        const int32_t* offs, int64_t T, int k, int64_t H, int E, char* dY, void* dW) {
+  dim3 grid((unsigned)((T + kBwdWaves - 1) / kBwdWaves)), block(kBwdWaves * 64);
+  hipStream_t s = (hipStream_t)stream;
+  if (k == 8)
+    hipLaunchKernelGGL((combine_bwd_kernel<DT, 8>), grid, block, 0, s, dout, Y, slot_to_row, wts, offs, T, k, H, E, dY, dW);
+  else if (k == 2)
+    hipLaunchKernelGGL((combine_bwd_kernel<DT, 2>), grid, block, 0, s, dout, Y, slot_to_row, wts, offs, T, k, H, E, dY, dW);
+  else if (k == 4)
+    hipLaunchKernelGGL((combine_bwd_kernel<DT, 4>), grid, block, 0, s, dout, Y, slot_to_row, wts, offs, T, k, H, E, dY, dW);
+  else
+    hipLaunchKernelGGL((combine_bwd_kernel<DT, 0>), grid, block, 0, s, dout, Y, slot_to_row, wts, offs, T, k, H, E, dY, dW);
+}
+
 template <int DT>
 void launch_combine(dim3 grid, dim3 block, void* stream, const char* Y, const int32_t* slot_to_row, const void* wts,
                     const int32_t* offs, int64_t T, int k, int64_t H, int E, char* O) {
@@ -187,6 +304,33 @@ extern "C" int hrm_moe_combine(const void* expert_out, const int32_t* slot_to_ro
   else
     hrm::launch_combine<HRM_MOE_F32>(grid, block, stream, Y, slot_to_row, topk_weight, expert_offsets, num_tokens,
                                      top_k, hidden_size, num_experts, O);
+  const hipError_t err = hipGetLastError();
+  if (err != hipSuccess) return (int)err;
+  return HRM_MOE_OK;
+}
+
+extern "C" int hrm_moe_combine_backward(const void* grad_out, const void* expert_out, const int32_t* slot_to_row,
+                                        const void* topk_weight, const int32_t* expert_offsets, int64_t num_tokens,
+                                        int32_t top_k, int64_t hidden_size, int32_t num_experts, int dtype,
+                                        void* grad_expert_out, void* grad_weight, void* stream) {
+  if (num_tokens < 0 || top_k < 1 || hidden_size < 1 || num_experts < 1) return HRM_MOE_ERR_INVALID;
+  if (dtype < HRM_MOE_BF16 || dtype > HRM_MOE_F32) return HRM_MOE_ERR_DTYPE;
+  if (top_k > hrm::kMaxTopK || hidden_size % 8 || hidden_size / 8 > (int64_t(1) << 27)) return HRM_MOE_ERR_UNSUPPORTED;
+  if (num_tokens == 0) return HRM_MOE_OK;
+  if (!grad_out || !expert_out || !slot_to_row || !topk_weight || !expert_offsets || !grad_expert_out || !grad_weight)
+    return HRM_MOE_ERR_INVALID;
+  const char* G = static_cast<const char*>(grad_out);
+  const char* Y = static_cast<const char*>(expert_out);
+  char* DY = static_cast<char*>(grad_expert_out);
+  if (dtype == HRM_MOE_BF16)
+    hrm::launch_combine_bwd<HRM_MOE_BF16>(stream, G, Y, slot_to_row, topk_weight, expert_offsets, num_tokens, top_k,
+                                          hidden_size, num_experts, DY, grad_weight);
+  else if (dtype == HRM_MOE_F16)
+    hrm::launch_combine_bwd<HRM_MOE_F16>(stream, G, Y, slot_to_row, topk_weight, expert_offsets, num_tokens, top_k,
+                                         hidden_size, num_experts, DY, grad_weight);
+  else
+    hrm::launch_combine_bwd<HRM_MOE_F32>(stream, G, Y, slot_to_row, topk_weight, expert_offsets, num_tokens, top_k,
+                                         hidden_size, num_experts, DY, grad_weight);
   const hipError_t err = hipGetLastError();
   if (err != hipSuccess) return (int)err;
   return HRM_MOE_OK;

@@ -37,6 +37,14 @@ constexpr int kBK = 64;
 constexpr int kMaxExperts = 1024;
 
 enum { KIND_NT = 0, KIND_GATHER_SWIGLU = 1, KIND_NN = 2 };
+// Epilogue modes of the DMA kernels (training path):
+//   EPI_PLAIN       store C
+//   EPI_SAVE_GU     gate/up kernel: also store the rounded gate and up values
+//                   (the reference's gate_up tensor, models/layers.py:326) to aux [M, 2N]
+//   EPI_SWIGLU_BWD  NN kernel computing dAct = dY . W_dn[e]: apply the backward of
+//                   silu(gate) * up (models/layers.py:328-329) with gate/up read from
+//                   aux [M, 2N] and store d(gate_up) [M, 2N] to C
+enum { EPI_PLAIN = 0, EPI_SAVE_GU = 1, EPI_SWIGLU_BWD = 2 };
 
 struct MTile {
   int32_t expert, row_start, row_end, pad;
@@ -573,6 +581,24 @@ __device__ __forceinline__ float swiglu_fast(float g, float u) {
   return sl * ur;
 }
 
+// Backward of silu(g) * u for one element, with the reference's rounding
+// points (torch autograd on 16-bit tensors): the saved silu output is rounded,
+// d_up = da * silu(g) and d_silu = da * u are rounded products, and silu's
+// backward is computed in fp32 as d_silu * sig * (1 + g * (1 - sig)) and rounded.
+template <typename TR>
+__device__ __forceinline__ void swiglu_bwd(float da, float g, float u, float& dg, float& du) {
+  const float den = 1.0f + expf(-g);
+  const float sig = 1.0f / den;
+  const float sl = TR::to_f(TR::from_f(g / den));
+  du = TR::to_f(TR::from_f(da * sl));
+  const float ds = TR::to_f(TR::from_f(da * u));
+  dg = TR::to_f(TR::from_f(ds * sig * (1.0f + g * (1.0f - sig))));
+}
+
+__device__ __forceinline__ u32x4 bload16(__amdgpu_buffer_rsrc_t r, uint32_t voff) {
+  return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, voff, 0, 0));
+}
+
 __device__ __forceinline__ void bstore8(__amdgpu_buffer_rsrc_t r, uint32_t voff, u32x2 v) {
   __builtin_amdgcn_raw_buffer_store_b64(v, r, voff, 0, 0);
 }
@@ -589,13 +615,17 @@ __device__ __forceinline__ void bstore16(__amdgpu_buffer_rsrc_t r, uint32_t voff
 // stores and no branch is taken.
 // 4-wave variants are sized for two workgroups per CU (at most 256 registers
 // per lane, two waves per SIMD); 8-wave variants run one per CU.
-template <typename TR, int KIND, int BM, int BN, int STAGES, int NW, int BK>
+template <typename TR, int KIND, int BM, int BN, int STAGES, int NW, int BK, int EPI = EPI_PLAIN>
 __global__ __launch_bounds__(NW * 64, NW == 4 ? 2 : 1) void mgemm_dma_kernel(const uint16_t* __restrict__ A,
                                                                const int32_t* __restrict__ gather,
                                                                const uint16_t* __restrict__ W,
                                                                uint16_t* __restrict__ C,
                                                                const int64_t* __restrict__ tpe, int E, int M, int N,
-                                                               int K, int tiles_n, uint32_t a_bytes) {
+                                                               int K, int tiles_n, uint32_t a_bytes,
+                                                               uint16_t* __restrict__ aux) {
+  static_assert(EPI == EPI_PLAIN || (EPI == EPI_SAVE_GU && KIND == KIND_GATHER_SWIGLU) ||
+                    (EPI == EPI_SWIGLU_BWD && KIND == KIND_NN),
+                "epilogue mode does not fit the kernel kind");
   constexpr int WGN = NW / 2;                                // waves along N (two along M)
   constexpr int MB = BM / 64;                                // 32-row blocks per wave
   constexpr int NB = BN / WGN / 32;                          // 32-column blocks per wave
@@ -888,7 +918,14 @@ __global__ __launch_bounds__(NW * 64, NW == 4 ? 2 : 1) void mgemm_dma_kernel(con
     // so both the 8-byte writes and the 16-byte read-back are conflict-free.
     const int c_rs = __builtin_amdgcn_readfirstlane(comp_rs);
     const int c_rows = __builtin_amdgcn_readfirstlane(comp_re - comp_rs);
-    const __amdgpu_buffer_rsrc_t rC = make_rsrc(C + (int64_t)c_rs * N, (uint32_t)c_rows * (uint32_t)N * 2);
+    // C rows hold N values, or 2N for the d(gate_up) output of EPI_SWIGLU_BWD;
+    // aux rows (gate/up) hold 2N
+    constexpr int CMUL = EPI == EPI_SWIGLU_BWD ? 2 : 1;
+    const __amdgpu_buffer_rsrc_t rC =
+        make_rsrc(C + (int64_t)c_rs * N * CMUL, (uint32_t)c_rows * (uint32_t)N * 2 * CMUL);
+    const __amdgpu_buffer_rsrc_t rX = EPI == EPI_PLAIN
+                                          ? rC
+                                          : make_rsrc(aux + (int64_t)c_rs * N * 2, (uint32_t)c_rows * (uint32_t)N * 4);
     constexpr int WCOLS = KIND == KIND_GATHER_SWIGLU ? BN / 2 / WGN : BN / WGN;  // output columns per wave
     constexpr int PITCH = WCOLS * 2;                                      // staged row bytes
     constexpr int C8 = PITCH / 8;                                         // 8-byte chunks per row
@@ -898,43 +935,73 @@ __global__ __launch_bounds__(NW * 64, NW == 4 ? 2 : 1) void mgemm_dma_kernel(con
     constexpr int APP = FIT >= 4 && MBH >= 4 ? 4 : (FIT >= 2 && MBH >= 2 ? 2 : 1);  // blocks per pass
     constexpr int LPR = PITCH / 16;                                       // read-back lanes per row
     constexpr int RPI = 64 / LPR;                                         // rows per read-back
+    constexpr int NPASS = EPI == EPI_SAVE_GU ? 3 : 1;                     // act, then gate, then up
     static_assert(FIT >= 1 && MBH % APP == 0 && RP * C8 == 32, "staging layout");
     char* stg = smem + ((g0 + nk - 1) % STAGES) * STAGE_BYTES + wave * REGION;
     const int col0 = comp_n0 + (KIND == KIND_GATHER_SWIGLU ? col_blk : wn * WCOLS);
     barrier_lds();
 #pragma unroll
-    for (int a0 = 0; a0 < MBH; a0 += APP) {
+    for (int pass = 0; pass < NPASS; ++pass) {
 #pragma unroll
-      for (int a = a0; a < a0 + APP; ++a) {
-        const int r = (a - a0) * 32 + (lane & 31);
-        const int g = (r / RP) % C8;
+      for (int a0 = 0; a0 < MBH; a0 += APP) {
 #pragma unroll
-        for (int b = 0; b < WCOLS / 32; ++b)
+        for (int a = a0; a < a0 + APP; ++a) {
+          const int r = (a - a0) * 32 + (lane & 31);
+          const int g = (r / RP) % C8;
 #pragma unroll
-          for (int gq = 0; gq < 4; ++gq) {
-            float o[4];
+          for (int b = 0; b < WCOLS / 32; ++b)
 #pragma unroll
-            for (int q = 0; q < 4; ++q) {
-              if constexpr (KIND == KIND_GATHER_SWIGLU)
-                o[q] = swiglu_fast<TR>(acc[b][a][gq * 4 + q], acc[b + NB / 2][a][gq * 4 + q]);
-              else
-                o[q] = acc[b][a][gq * 4 + q];
+            for (int gq = 0; gq < 4; ++gq) {
+              float o[4];
+#pragma unroll
+              for (int q = 0; q < 4; ++q) {
+                if constexpr (KIND == KIND_GATHER_SWIGLU) {
+                  const float x = acc[b][a][gq * 4 + q], y = acc[b + NB / 2][a][gq * 4 + q];
+                  o[q] = pass == 0 ? swiglu_fast<TR>(x, y) : (pass == 1 ? x : y);
+                } else {
+                  o[q] = acc[b][a][gq * 4 + q];
+                }
+              }
+              const int ch8 = (b * 32 + gq * 8) / 4 + (lane >> 5);
+              *reinterpret_cast<u32x2*>(stg + r * PITCH + ((ch8 ^ g) << 3)) = pack4<TR>(o[0], o[1], o[2], o[3]);
             }
-            const int ch8 = (b * 32 + gq * 8) / 4 + (lane >> 5);
-            *reinterpret_cast<u32x2*>(stg + r * PITCH + ((ch8 ^ g) << 3)) = pack4<TR>(o[0], o[1], o[2], o[3]);
-          }
-      }
+        }
 #pragma unroll
-      for (int i = 0; i < APP * 32 / RPI; ++i) {
-        const int r = i * RPI + lane / LPR;
-        const int c16 = lane % LPR;
-        const int g = (r / RP) % C8;
-        u32x4 v = *reinterpret_cast<const u32x4*>(stg + r * PITCH + ((c16 ^ (g >> 1)) << 4));
-        if (g & 1) v = u32x4{v[2], v[3], v[0], v[1]};
-        const uint32_t ml = (uint32_t)(row_base + a0 * 32 + r);
-        const int c = col0 + c16 * 8;
-        const uint32_t voff = c < N ? (ml * (uint32_t)N + (uint32_t)c) * 2 : 0x80000000u;
-        bstore16(rC, voff, v);
+        for (int i = 0; i < APP * 32 / RPI; ++i) {
+          const int r = i * RPI + lane / LPR;
+          const int c16 = lane % LPR;
+          const int g = (r / RP) % C8;
+          u32x4 v = *reinterpret_cast<const u32x4*>(stg + r * PITCH + ((c16 ^ (g >> 1)) << 4));
+          if (g & 1) v = u32x4{v[2], v[3], v[0], v[1]};
+          const uint32_t ml = (uint32_t)(row_base + a0 * 32 + r);
+          const int c = col0 + c16 * 8;
+          if constexpr (EPI == EPI_SWIGLU_BWD) {
+            // v holds dAct (rounded); gate and up of the same elements come from aux
+            const uint32_t xoff = c < N ? (ml * (uint32_t)N * 2 + (uint32_t)c) * 2 : 0x80000000u;
+            const u32x4 gv = bload16(rX, xoff), uv = bload16(rX, xoff + (uint32_t)N * 2);
+            u32x4 dgv, duv;
+#pragma unroll
+            for (int h2 = 0; h2 < 4; ++h2) {
+              float dg0, du0, dg1, du1;
+              swiglu_bwd<TR>(TR::to_f((uint16_t)(v[h2] & 0xffff)), TR::to_f((uint16_t)(gv[h2] & 0xffff)),
+                             TR::to_f((uint16_t)(uv[h2] & 0xffff)), dg0, du0);
+              swiglu_bwd<TR>(TR::to_f((uint16_t)(v[h2] >> 16)), TR::to_f((uint16_t)(gv[h2] >> 16)),
+                             TR::to_f((uint16_t)(uv[h2] >> 16)), dg1, du1);
+              dgv[h2] = pack2(TR::from_f(dg0), TR::from_f(dg1));
+              duv[h2] = pack2(TR::from_f(du0), TR::from_f(du1));
+            }
+            bstore16(rC, xoff, dgv);
+            bstore16(rC, xoff + (uint32_t)N * 2, duv);
+          } else if (pass == 0) {
+            const uint32_t voff = c < N ? (ml * (uint32_t)N + (uint32_t)c) * 2 : 0x80000000u;
+            bstore16(rC, voff, v);
+          } else {
+            // EPI_SAVE_GU: gate to columns [0, N), up to [N, 2N) of aux
+            const uint32_t xoff =
+                c < N ? (ml * (uint32_t)N * 2 + (uint32_t)c + (pass == 2 ? (uint32_t)N : 0u)) * 2 : 0x80000000u;
+            bstore16(rX, xoff, v);
+          }
+        }
       }
     }
   };
@@ -1406,12 +1473,12 @@ int launch_mgemm(const void* A, const int32_t* gather, const void* W, const int6
   return HRM_MOE_OK;
 }
 
-template <typename TR, int KIND, int BM, int BN, int STAGES, int NW, int BK>
+template <typename TR, int KIND, int BM, int BN, int STAGES, int NW, int BK, int EPI = EPI_PLAIN>
 int launch_mgemm_dma(const void* A, const int32_t* gather, const void* W, const int64_t* tpe, int64_t M, int N,
-                     int K, int E, int64_t a_rows, void* C, void* workspace, void* stream) {
+                     int K, int E, int64_t a_rows, void* C, void* workspace, void* stream, void* aux = nullptr) {
   (void)workspace;  // the DMA kernels plan their tiles themselves
   const int tiles_n = KIND == KIND_GATHER_SWIGLU ? (N + BN / 2 - 1) / (BN / 2) : (N + BN - 1) / BN;
-  auto kern = mgemm_dma_kernel<TR, KIND, BM, BN, STAGES, NW, BK>;
+  auto kern = mgemm_dma_kernel<TR, KIND, BM, BN, STAGES, NW, BK, EPI>;
   const size_t plan_bytes = sizeof(int) * 3 * (size_t)E;
   static int grid = 0, grid_e = -1;
   if (grid == 0 || grid_e != E) {
@@ -1419,7 +1486,7 @@ int launch_mgemm_dma(const void* A, const int32_t* gather, const void* W, const 
     grid_e = E;
   }
   HRM_LAUNCH(kern, dim3(grid), dim3(NW * 64), plan_bytes, stream, (const uint16_t*)A, gather, (const uint16_t*)W,
-             (uint16_t*)C, tpe, E, (int)M, N, K, tiles_n, (uint32_t)(a_rows * K * 2));
+             (uint16_t*)C, tpe, E, (int)M, N, K, tiles_n, (uint32_t)(a_rows * K * 2), (uint16_t*)aux);
   return HRM_MOE_OK;
 }
 
@@ -1518,6 +1585,33 @@ int dispatch_mgemm_t(const void* A, const int32_t* gather, const void* W, const 
   if (c.stages == 3) HRM_MG(128, 128, 3, 4, 64);
   HRM_MG(128, 128, 2, 4, 64);
 #undef HRM_MG
+}
+
+// Training-path epilogues (EPI_SAVE_GU, EPI_SWIGLU_BWD): DMA kernels only,
+// on the two default tile shapes.
+template <typename TR, int KIND, int EPI>
+int dispatch_mgemm_epi_t(const void* A, const int32_t* gather, const void* W, const int64_t* tpe, int64_t M, int N,
+                         int K, int E, int64_t a_rows, void* C, void* aux, void* stream) {
+  const int64_t w_rows = KIND == KIND_GATHER_SWIGLU ? 2 * (int64_t)N : (KIND == KIND_NN ? (int64_t)K : (int64_t)N);
+  const int64_t w_cols = KIND == KIND_NN ? (int64_t)N : (int64_t)K;
+  const int64_t c_cols = EPI == EPI_SWIGLU_BWD ? 2 * (int64_t)N : (int64_t)N;
+  if (K % kBK != 0 || a_rows * K * 2 >= (int64_t(1) << 32) || w_rows * w_cols * 2 >= (int64_t(1) << 32) ||
+      M * 2 * (int64_t)N * 2 >= (int64_t(1) << 32) || M * c_cols * 2 >= (int64_t(1) << 32))
+    return HRM_MOE_ERR_UNSUPPORTED;
+  const MCfg c = mgemm_cfg(M, E, KIND == KIND_GATHER_SWIGLU ? 2 * (int64_t)N : (int64_t)N, KIND == KIND_GATHER_SWIGLU);
+  if (c.bm == 256 && c.bn == 256 && c.waves == 8 && c.bk == 64 && c.stages == 2)
+    return launch_mgemm_dma<TR, KIND, 256, 256, 2, 8, 64, EPI>(A, gather, W, tpe, M, N, K, E, a_rows, C, nullptr,
+                                                               stream, aux);
+  return launch_mgemm_dma<TR, KIND, 128, 128, 2, 4, 64, EPI>(A, gather, W, tpe, M, N, K, E, a_rows, C, nullptr, stream,
+                                                             aux);
+}
+
+template <int KIND, int EPI>
+int dispatch_mgemm_epi(int dtype, const void* A, const int32_t* gather, const void* W, const int64_t* tpe, int64_t M,
+                       int N, int K, int E, int64_t a_rows, void* C, void* aux, void* stream) {
+  if (dtype == HRM_MOE_BF16)
+    return dispatch_mgemm_epi_t<BF16, KIND, EPI>(A, gather, W, tpe, M, N, K, E, a_rows, C, aux, stream);
+  return dispatch_mgemm_epi_t<F16, KIND, EPI>(A, gather, W, tpe, M, N, K, E, a_rows, C, aux, stream);
 }
 
 template <int KIND>
@@ -1637,4 +1731,39 @@ extern "C" int hrm_moe_gate_up_swiglu(const void* hidden, const int32_t* sorted_
   return hrm::dispatch_mgemm<hrm::KIND_GATHER_SWIGLU>(dtype, hidden, sorted_token_idx, gate_up_weight,
                                                       tokens_per_expert, num_rows, (int)inter_size, (int)hidden_size,
                                                       num_experts, num_tokens, act, workspace, stream);
+}
+
+extern "C" int hrm_moe_gate_up_swiglu_save(const void* hidden, const int32_t* sorted_token_idx,
+                                           const int64_t* tokens_per_expert, const void* gate_up_weight,
+                                           int64_t num_tokens, int64_t num_rows, int64_t hidden_size,
+                                           int64_t inter_size, int32_t num_experts, int dtype, void* act,
+                                           void* gate_up, void* workspace, size_t workspace_bytes, void* stream) {
+  int st = hrm::check_common(num_rows, num_experts, dtype, workspace, workspace_bytes);
+  if (st) return st;
+  if (num_tokens < 0 || hidden_size < 1 || inter_size < 1) return HRM_MOE_ERR_INVALID;
+  if (hidden_size % 64 || inter_size % 8 || hidden_size >= (1 << 30) || inter_size >= (1 << 29))
+    return HRM_MOE_ERR_UNSUPPORTED;
+  if (num_rows == 0) return HRM_MOE_OK;
+  if (num_tokens == 0) return HRM_MOE_ERR_INVALID;
+  if (!hidden || !sorted_token_idx || !tokens_per_expert || !gate_up_weight || !act || !gate_up)
+    return HRM_MOE_ERR_INVALID;
+  return hrm::dispatch_mgemm_epi<hrm::KIND_GATHER_SWIGLU, hrm::EPI_SAVE_GU>(
+      dtype, hidden, sorted_token_idx, gate_up_weight, tokens_per_expert, num_rows, (int)inter_size, (int)hidden_size,
+      num_experts, num_tokens, act, gate_up, stream);
+}
+
+extern "C" int hrm_moe_down_dgrad_swiglu(const void* grad_expert_out, const void* down_weight,
+                                         const int64_t* tokens_per_expert, const void* gate_up, int64_t num_rows,
+                                         int64_t inter_size, int64_t hidden_size, int32_t num_experts, int dtype,
+                                         void* grad_gate_up, void* workspace, size_t workspace_bytes, void* stream) {
+  int st = hrm::check_common(num_rows, num_experts, dtype, workspace, workspace_bytes);
+  if (st) return st;
+  if (hidden_size < 1 || inter_size < 1) return HRM_MOE_ERR_INVALID;
+  if (hidden_size % 64 || inter_size % 8 || hidden_size >= (1 << 30) || inter_size >= (1 << 29))
+    return HRM_MOE_ERR_UNSUPPORTED;
+  if (num_rows == 0) return HRM_MOE_OK;
+  if (!grad_expert_out || !down_weight || !tokens_per_expert || !gate_up || !grad_gate_up) return HRM_MOE_ERR_INVALID;
+  return hrm::dispatch_mgemm_epi<hrm::KIND_NN, hrm::EPI_SWIGLU_BWD>(
+      dtype, grad_expert_out, nullptr, down_weight, tokens_per_expert, num_rows, (int)inter_size, (int)hidden_size,
+      num_experts, num_rows, grad_gate_up, const_cast<void*>(gate_up), stream);
 }

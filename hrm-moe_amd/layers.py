@@ -10,10 +10,16 @@ Forward paths (same arithmetic, same routing bits):
     grad): router kernel -> dispatch kernel -> fused gather + gate_up GEMM +
     SwiGLU -> down GEMM -> deterministic combine.  Five HIP launches plus the
     gate GEMM; no host synchronisation.
-  * autograd needed: the reference's grouped composition
-    (models/layers.py:311-334).  The router, dispatch and both grouped GEMMs
-    (forward, dgrad, wgrad) are the HIP kernels.  The gather, SwiGLU,
-    weighting and index_add_ are torch ops, so autograd covers them.
+  * autograd needed, hidden size a multiple of 64: the same forward kernels
+    (the gate/up kernel also saving the rounded gate/up values) inside one
+    autograd function whose backward is HIP too: combine backward, down dgrad
+    with the SwiGLU backward fused, both wgrads, gate_up dgrad and a
+    deterministic un-permute.  The router's softmax/top-k backward is torch
+    ops on [T, E].
+  * autograd needed, other hidden sizes: the reference's grouped composition
+    (models/layers.py:311-334) with the HIP router, dispatch and grouped GEMMs
+    (forward, dgrad, wgrad); gather, SwiGLU, weighting and index_add_ are
+    torch ops under autograd.
 """
 from __future__ import annotations
 
@@ -104,12 +110,65 @@ class _RouterTopK(torch.autograd.Function):
         return dz.to(ctx.logits_dtype), None, None, None
 
 
+class _GroupedExpertsFn(torch.autograd.Function):
+    """Grouped expert block (models/layers.py:317-334) with a HIP backward.
+
+    Forward: gather + gate_up GEMM + SwiGLU (saving the rounded gate/up values),
+    down GEMM, combine.  Backward, with the reference's rounding points:
+      combine backward   -> d_rows = round(dout[tok] * w), d_w = sum_h round(dout * rows)
+      down dgrad + SwiGLU backward (one kernel) -> d(gate_up)
+      down wgrad         -> dW_dn[e] = d_rows_e^T . act_e
+      gate_up dgrad      -> d_h_rows = d(gate_up) . W_gu[e]
+      un-permute         -> d_h[t] = sum over the token's rows (combine with unit weights,
+                            fp32 in row order: deterministic, unlike index_add_ on the device)
+      gate_up wgrad      -> dW_gu[e] = d(gate_up)_e^T . h[tok]_e
+    """
+
+    @staticmethod
+    def forward(ctx, hidden: Tensor, routing_weights: Tensor, gate_up_weight: Tensor, down_weight: Tensor,
+                d: "ops.Dispatch"):
+        act, gate_up = ops.gate_up_swiglu_save(hidden, d, gate_up_weight)
+        y = ops.grouped_gemm_nt(act, down_weight, d.tokens_per_expert)
+        out = ops.combine(y, d, routing_weights)
+        ctx.save_for_backward(hidden, routing_weights, gate_up_weight, down_weight, act, gate_up, y)
+        ctx.d = d
+        return out
+
+    @staticmethod
+    def backward(ctx, grad_out: Tensor):
+        hidden, routing_weights, gate_up_weight, down_weight, act, gate_up, y = ctx.saved_tensors
+        d = ctx.d
+        tpe = d.tokens_per_expert
+        need_h, need_w, need_gu, need_dn = ctx.needs_input_grad[:4]
+        grad_out = grad_out.to(hidden.dtype).contiguous()
+        d_rows, d_w = ops.combine_backward(grad_out, y, d, routing_weights)
+        d_dn = ops.grouped_gemm_tn(d_rows, act, tpe) if need_dn else None
+        d_h = d_gu_w = None
+        if need_h or need_gu:
+            d_gate_up = ops.down_dgrad_swiglu(d_rows, down_weight, tpe, gate_up)
+            if need_h:
+                d_h_rows = ops.grouped_gemm_nn(d_gate_up, gate_up_weight, tpe)
+                ones = torch.ones_like(routing_weights)
+                d_h = ops.combine(d_h_rows, d, ones)
+            if need_gu:
+                h_rows = hidden.index_select(0, d.sorted_token_idx.long())
+                d_gu_w = ops.grouped_gemm_tn(d_gate_up, h_rows, tpe)
+        return d_h, (d_w if need_w else None), d_gu_w, d_dn, None
+
+
 class SparseMoEGroupedExperts(nn.Module):
     """Expert weights and compute (models/layers.py:248-357, grouped branch).
 
     Parameters: ``gate_up_weight`` [E, 2I, H] (gate rows 0..I-1, up rows
     I..2I-1) and ``down_weight`` [E, H, I].
+
+    ``fused_backward`` (default True) selects the HIP backward of the whole
+    expert block when autograd is needed and the hidden size is a multiple of
+    64; False runs the reference's composition under autograd instead (same
+    forward values; used to compare the two).
     """
+
+    fused_backward = True
 
     def __init__(self, hidden_size: int, intermediate_size: int, num_experts: int, backend: str = "hip",
                  init_std_in=None, init_std_out=None, **kwargs):
@@ -154,6 +213,15 @@ class SparseMoEGroupedExperts(nn.Module):
             with record_moe_profile_phase("combine"):
                 return ops.combine(y, d, routing_weights)
 
+        if self.fused_backward and hidden_states.shape[1] % 64 == 0:
+            # HIP forward and backward of the whole expert block
+            with record_moe_profile_phase("dispatch"):
+                d = ops.permute(selected_experts, self.num_experts)
+            with record_moe_profile_phase("experts"):
+                return _GroupedExpertsFn.apply(hidden_states, routing_weights, gate_up_weight, down_weight, d)
+
+        # hidden sizes that are not a multiple of 64: the reference's composition,
+        # with the HIP grouped GEMMs under torch autograd
         with record_moe_profile_phase("dispatch"):
             d = ops.permute(selected_experts, self.num_experts, want_sort_idx=True)
             sorted_token_idx = d.sorted_token_idx.long()

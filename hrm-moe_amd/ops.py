@@ -226,3 +226,87 @@ def combine(expert_out: torch.Tensor, dispatch: Dispatch, topk_weight: torch.Ten
                                          _lib.dtype_code(expert_out.dtype), _lib.ptr(out), _lib.stream_of(dev))
     _lib.check(st, "combine")
     return out
+
+
+# ---------------------------------------------------------------------------
+# Training path: saved gate/up, fused SwiGLU backward, combine backward
+# (the quantities torch autograd computes for models/layers.py:317-334)
+# ---------------------------------------------------------------------------
+
+def gate_up_swiglu_save(hidden: torch.Tensor, dispatch: Dispatch, gate_up_weight: torch.Tensor):
+    """(act [R,I], gate_up [R,2I]): gate_up_swiglu that also returns the rounded gate/up values."""
+    dev = _require_cuda(hidden, gate_up_weight)
+    t, h = hidden.shape
+    e, two_i, wk = gate_up_weight.shape
+    if wk != h or two_i % 2:
+        raise ValueError(f"gate_up_weight {tuple(gate_up_weight.shape)} does not match hidden size {h}")
+    if gate_up_weight.dtype != hidden.dtype:
+        raise TypeError(f"dtype mismatch: hidden {hidden.dtype}, weight {gate_up_weight.dtype}")
+    dt = _gemm_dtype(hidden)
+    inter = two_i // 2
+    hidden, gate_up_weight = hidden.contiguous(), gate_up_weight.contiguous()
+    r = dispatch.sorted_token_idx.numel()
+    act = hidden.new_empty((r, inter))
+    gate_up = hidden.new_empty((r, two_i))
+    lib = _lib.lib()
+    ws = _workspace(lib.hrm_moe_grouped_gemm_workspace_size(r, e), dev)
+    with _lib.device_guard(dev):
+        st = lib.hrm_moe_gate_up_swiglu_save(_lib.ptr(hidden), _lib.ptr(dispatch.sorted_token_idx),
+                                             _lib.ptr(dispatch.tokens_per_expert), _lib.ptr(gate_up_weight), t, r, h,
+                                             inter, e, dt, _lib.ptr(act), _lib.ptr(gate_up), _lib.ptr(ws), ws.numel(),
+                                             _lib.stream_of(dev))
+    _lib.check(st, "gate_up_swiglu_save")
+    return act, gate_up
+
+
+def down_dgrad_swiglu(grad_expert_out: torch.Tensor, down_weight: torch.Tensor, tokens_per_expert: torch.Tensor,
+                      gate_up: torch.Tensor) -> torch.Tensor:
+    """d(gate_up) [R,2I]: dact = grad @ W_dn[e], then the backward of silu(gate) * up."""
+    dev = _require_cuda(grad_expert_out, down_weight, gate_up)
+    r, h = grad_expert_out.shape
+    e, wh, inter = down_weight.shape
+    if wh != h:
+        raise ValueError(f"down_weight {tuple(down_weight.shape)} does not match grad width {h}")
+    if gate_up.shape != (r, 2 * inter):
+        raise ValueError(f"gate_up {tuple(gate_up.shape)} is not [{r}, {2 * inter}]")
+    if down_weight.dtype != grad_expert_out.dtype or gate_up.dtype != grad_expert_out.dtype:
+        raise TypeError("dtype mismatch between grad, down_weight and gate_up")
+    dt = _gemm_dtype(grad_expert_out)
+    grad_expert_out, down_weight, gate_up = grad_expert_out.contiguous(), down_weight.contiguous(), gate_up.contiguous()
+    tpe = _tpe64(tokens_per_expert, dev)
+    if tpe.numel() != e:
+        raise ValueError(f"tokens_per_expert has {tpe.numel()} entries for {e} experts")
+    out = grad_expert_out.new_empty((r, 2 * inter))
+    lib = _lib.lib()
+    ws = _workspace(lib.hrm_moe_grouped_gemm_workspace_size(r, e), dev)
+    with _lib.device_guard(dev):
+        st = lib.hrm_moe_down_dgrad_swiglu(_lib.ptr(grad_expert_out), _lib.ptr(down_weight), _lib.ptr(tpe),
+                                           _lib.ptr(gate_up), r, inter, h, e, dt, _lib.ptr(out), _lib.ptr(ws),
+                                           ws.numel(), _lib.stream_of(dev))
+    _lib.check(st, "down_dgrad_swiglu")
+    return out
+
+
+def combine_backward(grad_out: torch.Tensor, expert_out: torch.Tensor, dispatch: Dispatch,
+                     topk_weight: torch.Tensor):
+    """(grad_expert_out [R,H], grad_weight [T,k]) of combine(expert_out, dispatch, topk_weight)."""
+    dev = _require_cuda(grad_out, expert_out, topk_weight)
+    t, k = topk_weight.shape
+    r, h = expert_out.shape
+    if r != t * k or grad_out.shape != (t, h):
+        raise ValueError(f"shapes: grad_out {tuple(grad_out.shape)}, expert_out {tuple(expert_out.shape)}, "
+                         f"weights {tuple(topk_weight.shape)}")
+    if not (grad_out.dtype == expert_out.dtype == topk_weight.dtype):
+        raise TypeError("combine_backward needs one dtype for grad_out, expert_out and weights")
+    grad_out, expert_out, topk_weight = grad_out.contiguous(), expert_out.contiguous(), topk_weight.contiguous()
+    e = dispatch.tokens_per_expert.numel()
+    grad_rows = expert_out.new_empty((r, h))
+    grad_w = topk_weight.new_empty((t, k))
+    with _lib.device_guard(dev):
+        st = _lib.lib().hrm_moe_combine_backward(_lib.ptr(grad_out), _lib.ptr(expert_out),
+                                                  _lib.ptr(dispatch.slot_to_row), _lib.ptr(topk_weight),
+                                                  _lib.ptr(dispatch.expert_offsets), t, k, h, e,
+                                                  _lib.dtype_code(expert_out.dtype), _lib.ptr(grad_rows),
+                                                  _lib.ptr(grad_w), _lib.stream_of(dev))
+    _lib.check(st, "combine_backward")
+    return grad_rows, grad_w

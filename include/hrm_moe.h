@@ -148,6 +148,48 @@ int hrm_moe_combine(const void* expert_out, const int32_t* slot_to_row, const vo
                     const int32_t* expert_offsets, int64_t num_tokens, int32_t top_k, int64_t hidden_size,
                     int32_t num_experts, int dtype, void* out, void* stream);
 
+/*
+ * Training path.  The reference differentiates the grouped composition of
+ * models/layers.py:317-334 with torch autograd; these entry points compute the
+ * same quantities with the reference's rounding points.
+ */
+
+/* hrm_moe_gate_up_swiglu, also storing the rounded gate and up values
+ * gate_up [R, 2I] (gate in columns [0,I), up in [I,2I)): the reference's
+ * gate_up tensor (models/layers.py:326), saved for the backward of
+ * silu(gate) * up.  Limits as hrm_moe_gate_up_swiglu, and H a multiple of 64. */
+int hrm_moe_gate_up_swiglu_save(const void* hidden, const int32_t* sorted_token_idx,
+                                const int64_t* tokens_per_expert, const void* gate_up_weight, int64_t num_tokens,
+                                int64_t num_rows, int64_t hidden_size, int64_t inter_size, int32_t num_experts,
+                                int dtype, void* act, void* gate_up, void* workspace, size_t workspace_bytes,
+                                void* stream);
+
+/* Down projection dgrad with the SwiGLU backward fused into its epilogue:
+ *   dact[r]        = round(grad_expert_out[r] . down_weight[e])    [R, I]
+ *   d_up[r,i]      = round(dact * round(silu(gate)))
+ *   d_gate[r,i]    = round(round(dact * up) * sig * (1 + gate * (1 - sig))),  sig = sigmoid(gate)
+ * written to grad_gate_up [R, 2I] as [d_gate | d_up].  This is the backward of
+ * triton_grouped_linear on down_weight (moe_triton_grouped_gemm.py:472) followed
+ * by torch autograd through silu(gate) * up (models/layers.py:328-329).
+ *   grad_expert_out [R,H], down_weight [E,H,I], gate_up [R,2I].
+ * Limits: H a multiple of 64, I a multiple of 8, E <= 1024. */
+int hrm_moe_down_dgrad_swiglu(const void* grad_expert_out, const void* down_weight, const int64_t* tokens_per_expert,
+                              const void* gate_up, int64_t num_rows, int64_t inter_size, int64_t hidden_size,
+                              int32_t num_experts, int dtype, void* grad_gate_up, void* workspace,
+                              size_t workspace_bytes, void* stream);
+
+/* Backward of the weighted combine (models/layers.py:333-334 under autograd):
+ *   grad_expert_out[slot_to_row[t*k+j]] = round(grad_out[t] * topk_weight[t,j])
+ *   grad_weight[t,j] = round(sum_h round(grad_out[t,h] * expert_out[row,h]))
+ * The sum over h is in fp32 with a fixed order, so results are deterministic.
+ * Slots with a dropped row (>= expert_offsets[E]) get grad_weight 0 and no
+ * row write.  grad_out [T,H], expert_out and grad_expert_out [R,H],
+ * topk_weight and grad_weight [T,k].  Limits: H a multiple of 8, 1 <= k <= 32. */
+int hrm_moe_combine_backward(const void* grad_out, const void* expert_out, const int32_t* slot_to_row,
+                             const void* topk_weight, const int32_t* expert_offsets, int64_t num_tokens,
+                             int32_t top_k, int64_t hidden_size, int32_t num_experts, int dtype,
+                             void* grad_expert_out, void* grad_weight, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -22,6 +22,9 @@ Pinning (what checks each function; tests/test_oracle.py):
   moe_forward     C1 golden (fp32, reference imported on CPU), bf16 golden at a
                   small shape, and the per-expert "origin" formulation
                   (models/layers.py:481-515) computed independently.
+  experts_vjp     float64 gradients equal those of the independent per-expert
+                  formulation and a central finite difference along a random
+                  direction.
   aux_loss        closed form vs C1 golden.
 """
 from __future__ import annotations
@@ -192,9 +195,10 @@ def grouped_linear(inp: torch.Tensor, weight: torch.Tensor, tpe) -> torch.Tensor
     e, n, wk = weight.shape
     if wk != k:
         raise ValueError(f"grouped GEMM K mismatch: input K={k}, weight K={wk}")
-    out = torch.zeros((m, n), dtype=torch.float32)
-    a32 = inp.float()
-    w32 = weight.float()
+    acc = torch.promote_types(inp.dtype, torch.float32)  # fp32, or float64 for float64 checks
+    out = torch.zeros((m, n), dtype=acc)
+    a32 = inp.to(acc)
+    w32 = weight.to(acc)
     for g, s, t in _groups(tpe):
         if t > s:
             out[s:t] = a32[s:t] @ w32[g].T
@@ -317,6 +321,38 @@ def moe_forward_origin(x: torch.Tensor, gate_weight: torch.Tensor, gate_up_weigh
         y = ((F.silu(gate) * up).float() @ down_weight[e].float().T).to(h.dtype)
         out.index_add_(0, tok, (y * w[tok, slot, None]).to(h.dtype))
     return out.reshape(shape)
+
+
+def experts_vjp(h: torch.Tensor, w: torch.Tensor, gate_up_weight: torch.Tensor, down_weight: torch.Tensor,
+                idx, grad_out: torch.Tensor) -> dict:
+    """Gradients of the grouped expert block by torch autograd on the CPU (models/layers.py:311-334).
+
+    The forward is the reference's composition in the tensors' dtype: stable
+    dispatch (:312-322), index_select of the hidden rows (:320), gate_up
+    grouped linear (:326), silu(gate) * up (:328-329), down grouped linear
+    (:331), weighting and index_add_ (:333-334); the grouped linears follow
+    the device op (fp32 accumulation, one rounding, moe_triton_grouped_gemm.py:
+    466-475 for the backward).  Returns d_hidden [T,H], d_weights [T,k],
+    d_gate_up_weight, d_down_weight and the forward intermediates.
+    """
+    h = h.detach().clone().requires_grad_(True)
+    w = w.detach().clone().requires_grad_(True)
+    wgu = gate_up_weight.detach().clone().requires_grad_(True)
+    wdn = down_weight.detach().clone().requires_grad_(True)
+    t = h.shape[0]
+    p = permute(np.asarray(idx), wgu.shape[0])
+    sorted_w = w.reshape(-1)[torch.from_numpy(p["sort_idx"])]
+    sorted_h = h.index_select(0, torch.from_numpy(p["sorted_token_idx"]))
+    gu = grouped_linear(sorted_h, wgu, p["tokens_per_expert"])
+    gu.retain_grad()
+    act = swiglu(gu)
+    y = grouped_linear(act, wdn, p["tokens_per_expert"])
+    y.retain_grad()
+    out = combine(y, sorted_w, p["sorted_token_idx"], t)
+    out.backward(grad_out.to(out.dtype))
+    return dict(out=out.detach(), d_hidden=h.grad, d_weights=w.grad, d_gate_up_weight=wgu.grad,
+                d_down_weight=wdn.grad, gate_up=gu.detach(), act=act.detach(), expert_out=y.detach(),
+                d_gate_up=gu.grad, d_expert_out=y.grad, **p)
 
 
 def load_balancing_loss(probs: torch.Tensor, idx: torch.Tensor, num_experts: int) -> torch.Tensor:

@@ -90,6 +90,29 @@ def test_grouped_gemm_rejects_bad_arguments():
     assert c(buf, buf, buf, buf, 16, 8, 256, 64, 9, buf, NULL) == _lib.ERR_DTYPE
 
 
+def test_training_entry_points_reject_bad_arguments():
+    lib = _lib.load()
+    ws = lib.hrm_moe_grouped_gemm_workspace_size(1024, 64)
+    buf = ctypes.c_void_p(1 << 20)  # never dereferenced: every call below returns before launching
+    s = lib.hrm_moe_gate_up_swiglu_save
+    assert s(buf, buf, buf, buf, 16, 128, 256, 64, 64, _lib.BF16, buf, buf, NULL, 0, NULL) == _lib.ERR_WORKSPACE
+    assert s(buf, buf, buf, buf, 16, 128, 96, 64, 64, _lib.BF16, buf, buf, buf, ws, NULL) == _lib.ERR_UNSUPPORTED
+    assert s(buf, buf, buf, buf, 16, 128, 256, 64, 64, _lib.F32, buf, buf, buf, ws, NULL) == _lib.ERR_DTYPE
+    assert s(buf, buf, buf, buf, 16, 128, 256, 64, 64, _lib.BF16, buf, NULL, buf, ws, NULL) == _lib.ERR_INVALID
+    assert s(buf, buf, buf, buf, 16, 0, 256, 64, 64, _lib.BF16, buf, buf, buf, ws, NULL) == _lib.OK
+    d = lib.hrm_moe_down_dgrad_swiglu
+    assert d(buf, buf, buf, buf, 128, 64, 200, 64, _lib.BF16, buf, buf, ws, NULL) == _lib.ERR_UNSUPPORTED
+    assert d(buf, buf, buf, buf, 128, 60, 256, 64, _lib.BF16, buf, buf, ws, NULL) == _lib.ERR_UNSUPPORTED
+    assert d(buf, buf, buf, NULL, 128, 64, 256, 64, _lib.BF16, buf, buf, ws, NULL) == _lib.ERR_INVALID
+    assert d(buf, buf, buf, buf, 0, 64, 256, 64, _lib.BF16, buf, buf, ws, NULL) == _lib.OK
+    b = lib.hrm_moe_combine_backward
+    assert b(buf, buf, buf, buf, buf, 16, 33, 256, 64, _lib.BF16, buf, buf, NULL) == _lib.ERR_UNSUPPORTED
+    assert b(buf, buf, buf, buf, buf, 16, 8, 252, 64, _lib.BF16, buf, buf, NULL) == _lib.ERR_UNSUPPORTED
+    assert b(buf, buf, buf, buf, buf, 16, 8, 256, 64, 9, buf, buf, NULL) == _lib.ERR_DTYPE
+    assert b(buf, buf, buf, buf, buf, 16, 8, 256, 64, _lib.BF16, buf, NULL, NULL) == _lib.ERR_INVALID
+    assert b(buf, buf, buf, buf, buf, 0, 8, 256, 64, _lib.BF16, buf, buf, NULL) == _lib.OK
+
+
 def test_check_maps_status_to_reference_exceptions():
     with pytest.raises(TypeError):
         _lib.check(_lib.ERR_DTYPE, "x")

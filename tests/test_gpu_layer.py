@@ -154,8 +154,12 @@ def _reference_training_loss(x, wg, wgu, wdn, k, idx, grad):
     return out, (x.grad, wg.grad, wgu.grad, wdn.grad)
 
 
-def test_training_path_forward_backward(cuda):
-    t, h, e, i, k = 512, 256, 8, 128, 2
+@pytest.mark.parametrize("t,h,e,i,k", [
+    (512, 256, 8, 128, 2),    # HIP backward of the expert block (hidden size a multiple of 64)
+    (512, 200, 8, 128, 2),    # reference composition under autograd (other hidden sizes)
+    (1024, 1280, 64, 448, 8),  # L shape, HIP backward
+])
+def test_training_path_forward_backward(cuda, t, h, e, i, k):
     layer, (x, wg, wgu, wdn) = build_layer(cuda, 6, t, h, e, i, k)
     grad = torch.from_numpy(synth.normal(61, (t, h))).to(BF)
     xg = x.to(cuda).requires_grad_(True)

@@ -11,6 +11,7 @@ import os
 import numpy as np
 import pytest
 import torch
+import torch.nn.functional as F
 
 from oracle import moe_oracle as mo
 from oracle import synth
@@ -279,3 +280,75 @@ def test_bf16_small_golden_bit_exact(c1):
     assert torch.equal(out, ref)
     assert np.array_equal(im["idx"].numpy(), c1["bf16s__idx"].astype(np.int64))
     assert np.array_equal(im["weights"].view(torch.int16).numpy().view(np.uint16), c1["bf16s__weights_bits"])
+
+
+# ------------------------------------------------------------ experts_vjp ----
+
+def test_experts_vjp_matches_c1_golden_weight_grads(c1):
+    """Expert weight gradients of the reference module itself (fp32, loss sum(out * grad) + aux)."""
+    (x, wg, wgu, wdn), k, e = _c1_inputs(c1)
+    t, h = x.shape
+    grad = torch.from_numpy(synth.normal(12, (t, h)))
+    _, w, idx = mo.router_topk(F.linear(x, wg), k, True, x.dtype)
+    r = mo.experts_vjp(x, w, wgu, wdn, idx.numpy(), grad)
+    assert torch.equal(r["out"], torch.from_numpy(c1["c1_grouped_triton__out"]))
+    for name, got in (("gate_up", r["d_gate_up_weight"]), ("down", r["d_down_weight"])):
+        want_rows = torch.from_numpy(c1[f"c1_grouped_triton__{name}_grad_e0_rows0_3"])
+        assert torch.allclose(got[0, :4], want_rows, rtol=1e-4, atol=1e-6), name
+        sq = float(got.double().pow(2).sum())
+        want_sq = float(c1[f"c1_grouped_triton__{name}_grad_sq_sum"])
+        assert abs(sq / want_sq - 1.0) < 1e-5, name
+
+
+def _origin_experts(h, w, wgu, wdn, idx):
+    """Per-expert loop (models/layers.py:497-506) on the given routing, differentiable."""
+    out = torch.zeros_like(h)
+    for e in range(wgu.shape[0]):
+        tok, slot = torch.where(idx == e)
+        if tok.numel() == 0:
+            continue
+        gate, up = (h[tok] @ wgu[e].T).chunk(2, dim=-1)
+        y = (F.silu(gate) * up) @ wdn[e].T
+        out = out.index_add(0, tok, y * w[tok, slot, None])
+    return out
+
+
+def test_experts_vjp_matches_origin_formulation_and_finite_differences():
+    t, h, e, i, k = 40, 24, 6, 16, 3
+    rng = np.random.default_rng(5)
+    idx = np.argsort(rng.random((t, e)), axis=1)[:, :k]
+    x, wgu, wdn, w, g = (torch.from_numpy(rng.standard_normal(s)).double() for s in
+                         ((t, h), (e, 2 * i, h), (e, h, i), (t, k), (t, h)))
+    wgu, wdn = wgu * 0.2, wdn * 0.2
+    r = mo.experts_vjp(x, w, wgu, wdn, idx, g)
+    leaves = [a.clone().requires_grad_(True) for a in (x, w, wgu, wdn)]
+    out = _origin_experts(*leaves, torch.from_numpy(idx))
+    assert torch.allclose(out, r["out"], rtol=1e-12, atol=1e-12)
+    out.backward(g)
+    for name, leaf in zip(("d_hidden", "d_weights", "d_gate_up_weight", "d_down_weight"), leaves):
+        assert torch.allclose(r[name], leaf.grad, rtol=1e-10, atol=1e-12), name
+    # directional derivative of <g, out> along a random direction of every input
+    dirs = [torch.from_numpy(rng.standard_normal(a.shape)) for a in (x, w, wgu, wdn)]
+    eps = 1e-6
+
+    def f(s):
+        return float((mo.experts_vjp(*(a + s * v for a, v in zip((x, w, wgu, wdn), dirs)), idx, g)["out"] * g).sum())
+
+    fd = (f(eps) - f(-eps)) / (2 * eps)
+    an = sum(float((r[n] * v).sum()) for n, v in zip(("d_hidden", "d_weights", "d_gate_up_weight",
+                                                       "d_down_weight"), dirs))
+    assert abs(fd - an) <= 1e-6 * max(1.0, abs(an))
+
+
+def test_experts_vjp_planted_wrong_swiglu_grad_is_caught():
+    """A transposed gate/up pairing in the backward would fail the origin comparison above:
+    check that the comparison discriminates by planting the swap in the forward weights."""
+    t, h, e, i, k = 16, 8, 3, 4, 2
+    rng = np.random.default_rng(9)
+    idx = np.argsort(rng.random((t, e)), axis=1)[:, :k]
+    x, wgu, wdn, w, g = (torch.from_numpy(rng.standard_normal(s)).double() for s in
+                         ((t, h), (e, 2 * i, h), (e, h, i), (t, k), (t, h)))
+    r = mo.experts_vjp(x, w, wgu, wdn, idx, g)
+    swapped = torch.cat([wgu[:, i:], wgu[:, :i]], dim=1)
+    r2 = mo.experts_vjp(x, w, swapped, wdn, idx, g)
+    assert not torch.allclose(r["d_hidden"], r2["d_hidden"], atol=1e-6)
