@@ -1512,7 +1512,7 @@ bool mcfg_built(const MCfg& c) {
     return (c.bk == 64 && c.stages == 2) || (c.bk == 32 && c.stages == 4);
   return false;
 }
-MCfg mgemm_cfg(int64_t M, int E, int64_t w_rows, bool gate_up) {
+MCfg mgemm_cfg(int64_t M, int E, int64_t w_rows, bool gate_up, bool nn = false) {
   const char* env = getenv("HRM_MOE_GEMM_CFG");  // read per call: tests switch variants in one process
   if (env && *env) {
     MCfg c{0, 0, 0, 4, 64};
@@ -1522,7 +1522,11 @@ MCfg mgemm_cfg(int64_t M, int E, int64_t w_rows, bool gate_up) {
   // The gate/up kernel stays on 128 x 128 tiles: its gathered rows measured
   // slower per cycle on 256 x 256 tiles even with half tiles balancing the
   // last N tile.
-  if (!gate_up && M >= (int64_t)E * 256 && w_rows % 256 == 0) return MCfg{256, 256, 2, 8, 64};
+  // The NN (dgrad) kernel takes 256 x 256 tiles even when its width is not a
+  // multiple of 256: at L's dact (N = 448) they measured 203 us against 272 us
+  // for 128 x 128 tiles, whose higher LDS and DMA traffic per flop costs more
+  // than the idle columns of the last N tile.
+  if (!gate_up && M >= (int64_t)E * 256 && (nn || w_rows % 256 == 0)) return MCfg{256, 256, 2, 8, 64};
   return MCfg{128, 128, 2, 4, 64};
 }
 
@@ -1561,7 +1565,8 @@ int dispatch_mgemm_t(const void* A, const int32_t* gather, const void* W, const 
       return HRM_MOE_OK;
     }
   }
-  MCfg c = mgemm_cfg(M, E, KIND == KIND_GATHER_SWIGLU ? 2 * (int64_t)N : (int64_t)N, KIND == KIND_GATHER_SWIGLU);
+  MCfg c = mgemm_cfg(M, E, KIND == KIND_GATHER_SWIGLU ? 2 * (int64_t)N : (int64_t)N, KIND == KIND_GATHER_SWIGLU,
+                     KIND == KIND_NN);
   if (K % c.bk != 0) c = MCfg{128, 128, 2, 4, 64};
   // the ring may run at most one tile ahead: STAGES - 1 <= K / BK
   if (c.stages - 1 > K / c.bk) {
@@ -1598,7 +1603,8 @@ int dispatch_mgemm_epi_t(const void* A, const int32_t* gather, const void* W, co
   if (K % kBK != 0 || a_rows * K * 2 >= (int64_t(1) << 32) || w_rows * w_cols * 2 >= (int64_t(1) << 32) ||
       M * 2 * (int64_t)N * 2 >= (int64_t(1) << 32) || M * c_cols * 2 >= (int64_t(1) << 32))
     return HRM_MOE_ERR_UNSUPPORTED;
-  const MCfg c = mgemm_cfg(M, E, KIND == KIND_GATHER_SWIGLU ? 2 * (int64_t)N : (int64_t)N, KIND == KIND_GATHER_SWIGLU);
+  const MCfg c = mgemm_cfg(M, E, KIND == KIND_GATHER_SWIGLU ? 2 * (int64_t)N : (int64_t)N, KIND == KIND_GATHER_SWIGLU,
+                           KIND == KIND_NN);
   if (c.bm == 256 && c.bn == 256 && c.waves == 8 && c.bk == 64 && c.stages == 2)
     return launch_mgemm_dma<TR, KIND, 256, 256, 2, 8, 64, EPI>(A, gather, W, tpe, M, N, K, E, a_rows, C, nullptr,
                                                                stream, aux);
