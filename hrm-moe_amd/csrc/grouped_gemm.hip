@@ -1149,12 +1149,20 @@ __global__ __launch_bounds__(256) void mgemm_skinny_kernel(const uint16_t* __res
 // over that XCD's contiguous eighth of the (expert, na-tile, nb-tile) list,
 // so an expert's rows stay in few L2s and ragged experts still balance.  The
 // epilogue is staged through the idle ring like the M-grouped kernels'.
-template <typename TR, int BA, int BB, int NW, int STAGES>
+// GB: the B operand's rows are gathered, B[b_index[row]] (B is [b_rows, Nb]),
+// as the gate_up wgrad reads the hidden rows of the expert's tokens.  Each lane
+// keeps the source rows of its k rows for the next step to be issued, loaded
+// one step ahead; the 2-stage ring's wait for all loads before each issue also
+// covers those index loads.
+template <typename TR, int BA, int BB, int NW, int STAGES, bool GB = false>
 __global__ __launch_bounds__(NW * 64, 1) void wgrad_dma8_kernel(const uint16_t* __restrict__ A,
                                                                 const uint16_t* __restrict__ B,
                                                                 uint16_t* __restrict__ C,
                                                                 const int* __restrict__ row_offsets, int E, int Na,
-                                                                int Nb, int* __restrict__ counters) {
+                                                                int Nb, int* __restrict__ counters,
+                                                                const int32_t* __restrict__ b_index,
+                                                                uint32_t b_bytes) {
+  static_assert(!GB || STAGES == 2, "gathered B needs the 2-stage ring (its issue waits for every load)");
   constexpr int WGN = NW / 2;
   constexpr int MB = BA / 64;             // 32-row (na) blocks per wave, 2 waves along na
   constexpr int NB = BB / WGN / 32;       // 32-column (nb) blocks per wave
@@ -1193,8 +1201,10 @@ __global__ __launch_bounds__(NW * 64, 1) void wgrad_dma8_kernel(const uint16_t* 
     const int rs = row_offsets[e], re = row_offsets[e + 1];
     const int nk = (re - rs + kBK - 1) / kBK;
     const __amdgpu_buffer_rsrc_t rA = make_rsrc(A + (int64_t)rs * Na, (uint32_t)(re - rs) * (uint32_t)Na * 2);
-    const __amdgpu_buffer_rsrc_t rB = make_rsrc(B + (int64_t)rs * Nb, (uint32_t)(re - rs) * (uint32_t)Nb * 2);
+    const __amdgpu_buffer_rsrc_t rB =
+        GB ? make_rsrc(B, b_bytes) : make_rsrc(B + (int64_t)rs * Nb, (uint32_t)(re - rs) * (uint32_t)Nb * 2);
     uint32_t oa[IA], ob[IB];
+    int gi[IB];  // GB: source row of each of this lane's B k rows in the next step to issue, -1 past the expert
 #pragma unroll
     for (int i = 0; i < IA; ++i) {
       const int kr = wave * KR + i * RPI_A + lane / LPR_A;
@@ -1209,8 +1219,16 @@ __global__ __launch_bounds__(NW * 64, 1) void wgrad_dma8_kernel(const uint16_t* 
       const int lc = (lane % LPR_B) ^ kr_swz(kr);
       int cb = b0 + lc * 8;
       cb = cb < Nb ? cb : Nb - 8;
-      ob[i] = ((uint32_t)kr * (uint32_t)Nb + (uint32_t)cb) * 2;
+      ob[i] = GB ? (uint32_t)cb * 2 : ((uint32_t)kr * (uint32_t)Nb + (uint32_t)cb) * 2;
     }
+    auto load_gi = [&](int kt) __attribute__((always_inline)) {
+#pragma unroll
+      for (int i = 0; i < IB; ++i) {
+        const int row = rs + kt * kBK + wave * KR + i * RPI_B + lane / LPR_B;
+        gi[i] = row < re ? b_index[row] : -1;
+      }
+    };
+    if constexpr (GB) load_gi(0);
     auto issue = [&](int kt, int stage) __attribute__((always_inline)) {
       char* sa = smem + stage * STAGE_BYTES;
       char* sb = sa + TA_BYTES;
@@ -1219,7 +1237,14 @@ __global__ __launch_bounds__(NW * 64, 1) void wgrad_dma8_kernel(const uint16_t* 
 #pragma unroll
       for (int i = 0; i < IA; ++i) dma16(rA, sa + (wave * KR + i * RPI_A) * (BA * 2), oa[i], sofa);
 #pragma unroll
-      for (int i = 0; i < IB; ++i) dma16(rB, sb + (wave * KR + i * RPI_B) * (BB * 2), ob[i], sofb);
+      for (int i = 0; i < IB; ++i) {
+        if constexpr (GB)
+          dma16(rB, sb + (wave * KR + i * RPI_B) * (BB * 2),
+                gi[i] >= 0 ? (uint32_t)gi[i] * (uint32_t)Nb * 2 + ob[i] : 0x80000000u, 0);
+        else
+          dma16(rB, sb + (wave * KR + i * RPI_B) * (BB * 2), ob[i], sofb);
+      }
+      if constexpr (GB) load_gi(kt + 1);
     };
 
     floatx16 acc[NB][MB];
@@ -1311,12 +1336,16 @@ __global__ __launch_bounds__(NW * 64, 1) void wgrad_dma8_kernel(const uint16_t* 
 
 // Wgrad fed by DMA: both operands are [64 rows][128 cols] tiles of the
 // expert's rows; rows past the expert's end read as zeros (buffer bounds).
-template <typename TR, int STAGES>
+// GB: gathered B rows, as in wgrad_dma8_kernel.
+template <typename TR, int STAGES, bool GB = false>
 __global__ __launch_bounds__(kThreads, 1) void wgrad_dma_kernel(const uint16_t* __restrict__ A,
                                                                const uint16_t* __restrict__ B,
                                                                uint16_t* __restrict__ C,
                                                                const int* __restrict__ row_offsets, int E, int Na,
-                                                               int Nb, int* __restrict__ work_counter) {
+                                                               int Nb, int* __restrict__ work_counter,
+                                                               const int32_t* __restrict__ b_index,
+                                                               uint32_t b_bytes) {
+  static_assert(!GB || STAGES == 2, "gathered B needs the 2-stage ring (its issue waits for every load)");
   constexpr int BA = 128, BB = 128;
   constexpr int MB = BA / 64, NB = BB / 64;
   constexpr int T_BYTES = kBK * 128 * 2;
@@ -1343,8 +1372,10 @@ __global__ __launch_bounds__(kThreads, 1) void wgrad_dma_kernel(const uint16_t* 
     const int rs = row_offsets[e], re = row_offsets[e + 1];
     const int nk = (re - rs + kBK - 1) / kBK;
     const __amdgpu_buffer_rsrc_t rA = make_rsrc(A + (int64_t)rs * Na, (uint32_t)(re - rs) * (uint32_t)Na * 2);
-    const __amdgpu_buffer_rsrc_t rB = make_rsrc(B + (int64_t)rs * Nb, (uint32_t)(re - rs) * (uint32_t)Nb * 2);
+    const __amdgpu_buffer_rsrc_t rB =
+        GB ? make_rsrc(B, b_bytes) : make_rsrc(B + (int64_t)rs * Nb, (uint32_t)(re - rs) * (uint32_t)Nb * 2);
     uint32_t oa[4], ob[4];
+    int gi[4];  // GB: source row of each of this lane's B k rows in the next step to issue, -1 past the expert
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int kr = wave * 16 + i * 4 + (lane >> 4);
@@ -1353,8 +1384,16 @@ __global__ __launch_bounds__(kThreads, 1) void wgrad_dma_kernel(const uint16_t* 
       ca = ca < Na ? ca : Na - 8;
       cb = cb < Nb ? cb : Nb - 8;
       oa[i] = ((uint32_t)kr * (uint32_t)Na + (uint32_t)ca) * 2;
-      ob[i] = ((uint32_t)kr * (uint32_t)Nb + (uint32_t)cb) * 2;
+      ob[i] = GB ? (uint32_t)cb * 2 : ((uint32_t)kr * (uint32_t)Nb + (uint32_t)cb) * 2;
     }
+    auto load_gi = [&](int kt) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int row = rs + kt * kBK + wave * 16 + i * 4 + (lane >> 4);
+        gi[i] = row < re ? b_index[row] : -1;
+      }
+    };
+    if constexpr (GB) load_gi(0);
     auto issue = [&](int kt, int stage) {
       char* sa = smem + stage * STAGE_BYTES;
       char* sb = sa + T_BYTES;
@@ -1363,8 +1402,13 @@ __global__ __launch_bounds__(kThreads, 1) void wgrad_dma_kernel(const uint16_t* 
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         dma16(rA, sa + (wave * 16 + i * 4) * 256, oa[i], sofa);
-        dma16(rB, sb + (wave * 16 + i * 4) * 256, ob[i], sofb);
+        if constexpr (GB)
+          dma16(rB, sb + (wave * 16 + i * 4) * 256,
+                gi[i] >= 0 ? (uint32_t)gi[i] * (uint32_t)Nb * 2 + ob[i] : 0x80000000u, 0);
+        else
+          dma16(rB, sb + (wave * 16 + i * 4) * 256, ob[i], sofb);
       }
+      if constexpr (GB) load_gi(kt + 1);
     };
 
     floatx16 acc[NB][MB];
@@ -1629,13 +1673,17 @@ int dispatch_mgemm(int dtype, const void* A, const int32_t* gather, const void* 
 
 template <typename TR>
 int launch_wgrad(const void* A, const void* B, const int64_t* tpe, int64_t M, int Na, int Nb, int E, void* C,
-                 void* workspace, void* stream) {
+                 void* workspace, void* stream, const int32_t* b_index = nullptr, int64_t b_rows = 0) {
   GemmWs w = carve(workspace, M, E, kBMMin);
   const int max_tiles = (int)((M + kBMMin - 1) / kBMMin + E);
   HRM_LAUNCH(plan_kernel, dim3(1), dim3(1024), 0, stream, tpe, E, M, kBMMin, w.tiles, max_tiles, w.count,
              w.row_offsets, w.work_counter);
-  const bool dma = M * (int64_t)Na * 2 < (int64_t(1) << 32) && M * (int64_t)Nb * 2 < (int64_t(1) << 32);
+  const bool gather = b_index != nullptr;
+  const int64_t b_span = gather ? b_rows : M;
+  const bool dma = M * (int64_t)Na * 2 < (int64_t(1) << 32) && b_span * (int64_t)Nb * 2 < (int64_t(1) << 32);
+  const uint32_t b_bytes = (uint32_t)(b_span * (int64_t)Nb * 2);
   if (!dma) {
+    if (gather) return HRM_MOE_ERR_UNSUPPORTED;  // operands beyond 32-bit buffer offsets
     auto kern = wgrad_kernel<TR, 128, 128>;
     static int grid = 0;
     if (grid == 0) grid = persistent_grid(kern);
@@ -1645,30 +1693,44 @@ int launch_wgrad(const void* A, const void* B, const int64_t* tpe, int64_t M, in
   }
   // 256 x 256 tiles with 8 waves when both widths fill them and experts have
   // enough rows to amortise a tile; HRM_MOE_WGRAD_STAGES=2|3 selects the
-  // 128 x 128 four-wave kernel instead.
+  // 128 x 128 four-wave kernel instead (gathered B: 2 stages).
   const char* env = getenv("HRM_MOE_WGRAD_STAGES");  // read per call: tests switch kernels in one process
   if (env && !*env) env = nullptr;
   if (!env && Na >= 256 && Nb >= 256 && M >= (int64_t)E * 256) {
-    auto kern = wgrad_dma8_kernel<TR, 256, 256, 8, 2>;
-    static int grid = 0;
-    if (grid == 0) grid = persistent_grid(kern, 512);
-    HRM_LAUNCH(kern, dim3(grid), dim3(512), 0, stream, (const uint16_t*)A, (const uint16_t*)B, (uint16_t*)C,
-               w.row_offsets, E, Na, Nb, w.work_counter);
+    if (gather) {
+      auto kern = wgrad_dma8_kernel<TR, 256, 256, 8, 2, true>;
+      static int grid = 0;
+      if (grid == 0) grid = persistent_grid(kern, 512);
+      HRM_LAUNCH(kern, dim3(grid), dim3(512), 0, stream, (const uint16_t*)A, (const uint16_t*)B, (uint16_t*)C,
+                 w.row_offsets, E, Na, Nb, w.work_counter, b_index, b_bytes);
+    } else {
+      auto kern = wgrad_dma8_kernel<TR, 256, 256, 8, 2>;
+      static int grid = 0;
+      if (grid == 0) grid = persistent_grid(kern, 512);
+      HRM_LAUNCH(kern, dim3(grid), dim3(512), 0, stream, (const uint16_t*)A, (const uint16_t*)B, (uint16_t*)C,
+                 w.row_offsets, E, Na, Nb, w.work_counter, nullptr, 0u);
+    }
     return HRM_MOE_OK;
   }
-  const int stages = env && atoi(env) == 2 ? 2 : 3;
-  if (stages == 2) {
+  const int stages = gather || (env && atoi(env) == 2) ? 2 : 3;
+  if (gather) {
+    auto kern = wgrad_dma_kernel<TR, 2, true>;
+    static int grid = 0;
+    if (grid == 0) grid = persistent_grid(kern);
+    HRM_LAUNCH(kern, dim3(grid), dim3(kThreads), 0, stream, (const uint16_t*)A, (const uint16_t*)B, (uint16_t*)C,
+               w.row_offsets, E, Na, Nb, w.work_counter, b_index, b_bytes);
+  } else if (stages == 2) {
     auto kern = wgrad_dma_kernel<TR, 2>;
     static int grid = 0;
     if (grid == 0) grid = persistent_grid(kern);
     HRM_LAUNCH(kern, dim3(grid), dim3(kThreads), 0, stream, (const uint16_t*)A, (const uint16_t*)B, (uint16_t*)C,
-               w.row_offsets, E, Na, Nb, w.work_counter);
+               w.row_offsets, E, Na, Nb, w.work_counter, nullptr, 0u);
   } else {
     auto kern = wgrad_dma_kernel<TR, 3>;
     static int grid = 0;
     if (grid == 0) grid = persistent_grid(kern);
     HRM_LAUNCH(kern, dim3(grid), dim3(kThreads), 0, stream, (const uint16_t*)A, (const uint16_t*)B, (uint16_t*)C,
-               w.row_offsets, E, Na, Nb, w.work_counter);
+               w.row_offsets, E, Na, Nb, w.work_counter, nullptr, 0u);
   }
   return HRM_MOE_OK;
 }
@@ -1772,4 +1834,20 @@ extern "C" int hrm_moe_down_dgrad_swiglu(const void* grad_expert_out, const void
   return hrm::dispatch_mgemm_epi<hrm::KIND_NN, hrm::EPI_SWIGLU_BWD>(
       dtype, grad_expert_out, nullptr, down_weight, tokens_per_expert, num_rows, (int)inter_size, (int)hidden_size,
       num_experts, num_rows, grad_gate_up, const_cast<void*>(gate_up), stream);
+}
+
+extern "C" int hrm_moe_grouped_gemm_tn_gather(const void* A, const void* B, const int32_t* b_row_index, int64_t b_rows,
+                                              const int64_t* tokens_per_expert, int64_t M, int64_t Na, int64_t Nb,
+                                              int32_t num_experts, int dtype, void* C, void* workspace,
+                                              size_t workspace_bytes, void* stream) {
+  int st = hrm::check_common(M, num_experts, dtype, workspace, workspace_bytes);
+  if (st) return st;
+  if (Na < 1 || Nb < 1 || b_rows < 0) return HRM_MOE_ERR_INVALID;
+  if (Na % 8 || Nb % 8 || Na >= (1 << 30) || Nb >= (1 << 30)) return HRM_MOE_ERR_UNSUPPORTED;
+  if (!tokens_per_expert || !C || (M > 0 && (!A || !B || !b_row_index || b_rows == 0))) return HRM_MOE_ERR_INVALID;
+  if (dtype == HRM_MOE_BF16)
+    return hrm::launch_wgrad<hrm::BF16>(A, B, tokens_per_expert, M, (int)Na, (int)Nb, num_experts, C, workspace,
+                                        stream, b_row_index, b_rows);
+  return hrm::launch_wgrad<hrm::F16>(A, B, tokens_per_expert, M, (int)Na, (int)Nb, num_experts, C, workspace, stream,
+                                     b_row_index, b_rows);
 }

@@ -121,7 +121,7 @@ class _GroupedExpertsFn(torch.autograd.Function):
       gate_up dgrad      -> d_h_rows = d(gate_up) . W_gu[e]
       un-permute         -> d_h[t] = sum over the token's rows (combine with unit weights,
                             fp32 in row order: deterministic, unlike index_add_ on the device)
-      gate_up wgrad      -> dW_gu[e] = d(gate_up)_e^T . h[tok]_e
+      gate_up wgrad      -> dW_gu[e] = d(gate_up)_e^T . h[tok]_e, the rows gathered by the kernel's DMA
     """
 
     @staticmethod
@@ -151,8 +151,7 @@ class _GroupedExpertsFn(torch.autograd.Function):
                 ones = torch.ones_like(routing_weights)
                 d_h = ops.combine(d_h_rows, d, ones)
             if need_gu:
-                h_rows = hidden.index_select(0, d.sorted_token_idx.long())
-                d_gu_w = ops.grouped_gemm_tn(d_gate_up, h_rows, tpe)
+                d_gu_w = ops.grouped_gemm_tn_gather(d_gate_up, hidden, d.sorted_token_idx, tpe)
         return d_h, (d_w if need_w else None), d_gu_w, d_dn, None
 
 

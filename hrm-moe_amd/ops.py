@@ -180,6 +180,31 @@ def grouped_gemm_tn(a: torch.Tensor, b: torch.Tensor, tokens_per_expert: torch.T
     return c
 
 
+def grouped_gemm_tn_gather(a: torch.Tensor, b: torch.Tensor, b_row_index: torch.Tensor,
+                           tokens_per_expert: torch.Tensor) -> torch.Tensor:
+    """C[e][Na,Nb] = A[rows_e]^T @ B[b_row_index[rows_e]]: wgrad over gathered B rows (B [b_rows, Nb])."""
+    dev = _require_cuda(a, b, b_row_index)
+    m, na = a.shape
+    b_rows, nb = b.shape
+    if b_row_index.shape != (m,):
+        raise ValueError(f"b_row_index has shape {tuple(b_row_index.shape)}, expected ({m},)")
+    if b.dtype != a.dtype:
+        raise TypeError(f"grouped wgrad dtype mismatch: {a.dtype} vs {b.dtype}")
+    dt = _gemm_dtype(a)
+    a, b = a.contiguous(), b.contiguous()
+    idx = b_row_index.to(torch.int32).contiguous()
+    tpe = _tpe64(tokens_per_expert, dev)
+    e = tpe.numel()
+    c = a.new_empty((e, na, nb))
+    lib = _lib.lib()
+    ws = _workspace(lib.hrm_moe_grouped_gemm_workspace_size(m, e), dev)
+    with _lib.device_guard(dev):
+        st = lib.hrm_moe_grouped_gemm_tn_gather(_lib.ptr(a), _lib.ptr(b), _lib.ptr(idx), b_rows, _lib.ptr(tpe), m, na,
+                                                nb, e, dt, _lib.ptr(c), _lib.ptr(ws), ws.numel(), _lib.stream_of(dev))
+    _lib.check(st, "grouped_gemm_tn_gather")
+    return c
+
+
 # ---------------------------------------------------------------------------
 # Fused expert projections (models/layers.py:318-334)
 # ---------------------------------------------------------------------------

@@ -190,6 +190,18 @@ int hrm_moe_combine_backward(const void* grad_out, const void* expert_out, const
                              int32_t top_k, int64_t hidden_size, int32_t num_experts, int dtype,
                              void* grad_expert_out, void* grad_weight, void* stream);
 
+/* hrm_moe_grouped_gemm_tn with the B operand's rows gathered:
+ *   C[e][Na,Nb] = A[rows_e]^T . B[b_row_index[rows_e]]
+ * with B [b_rows, Nb] and b_row_index [M] (values in [0, b_rows); others read
+ * as zero rows).  This is the gate_up grad_weight of the reference
+ * (moe_triton_grouped_gemm.py:474 on the rows index_select-ed at
+ * models/layers.py:320) without materialising the gathered rows.
+ * Limits as hrm_moe_grouped_gemm_tn, and b_rows * Nb * 2 < 2^32. */
+int hrm_moe_grouped_gemm_tn_gather(const void* A, const void* B, const int32_t* b_row_index, int64_t b_rows,
+                                   const int64_t* tokens_per_expert, int64_t M, int64_t Na, int64_t Nb,
+                                   int32_t num_experts, int dtype, void* C, void* workspace, size_t workspace_bytes,
+                                   void* stream);
+
 #ifdef __cplusplus
 }
 #endif

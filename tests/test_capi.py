@@ -105,6 +105,11 @@ def test_training_entry_points_reject_bad_arguments():
     assert d(buf, buf, buf, buf, 128, 60, 256, 64, _lib.BF16, buf, buf, ws, NULL) == _lib.ERR_UNSUPPORTED
     assert d(buf, buf, buf, NULL, 128, 64, 256, 64, _lib.BF16, buf, buf, ws, NULL) == _lib.ERR_INVALID
     assert d(buf, buf, buf, buf, 0, 64, 256, 64, _lib.BF16, buf, buf, ws, NULL) == _lib.OK
+    tg = lib.hrm_moe_grouped_gemm_tn_gather
+    assert tg(buf, buf, buf, 100, buf, 1024, 256, 252, 64, _lib.BF16, buf, buf, ws, NULL) == _lib.ERR_UNSUPPORTED
+    assert tg(buf, buf, NULL, 100, buf, 1024, 256, 256, 64, _lib.BF16, buf, buf, ws, NULL) == _lib.ERR_INVALID
+    assert tg(buf, buf, buf, -1, buf, 1024, 256, 256, 64, _lib.BF16, buf, buf, ws, NULL) == _lib.ERR_INVALID
+    assert tg(buf, buf, buf, 100, buf, 1024, 256, 256, 64, _lib.F32, buf, buf, ws, NULL) == _lib.ERR_DTYPE
     b = lib.hrm_moe_combine_backward
     assert b(buf, buf, buf, buf, buf, 16, 33, 256, 64, _lib.BF16, buf, buf, NULL) == _lib.ERR_UNSUPPORTED
     assert b(buf, buf, buf, buf, buf, 16, 8, 252, 64, _lib.BF16, buf, buf, NULL) == _lib.ERR_UNSUPPORTED

@@ -111,6 +111,40 @@ def test_grouped_gemm_tn(cuda, m, na, nb, e, dtype, pattern):
         assert torch.count_nonzero(got[torch.from_numpy(empty).to(cuda)]) == 0
 
 
+GATHER_TN_CASES = [
+    # m, na, nb, e, b_rows, dtype, kernel (HRM_MOE_WGRAD_STAGES: "" picks 256 x 256 where it fits)
+    (1000, 256, 512, 8, 300, torch.bfloat16, ""),
+    (777, 136, 200, 5, 777, torch.float16, ""),
+    (16384, 896, 1280, 64, 2048, torch.bfloat16, ""),
+    (16384, 896, 1280, 64, 2048, torch.bfloat16, "2"),
+    (4096, 512, 768, 4, 100, torch.bfloat16, ""),
+]
+
+
+@pytest.mark.parametrize("m,na,nb,e,b_rows,dtype,kernel", GATHER_TN_CASES)
+def test_grouped_gemm_tn_gather(cuda, m, na, nb, e, b_rows, dtype, kernel):
+    """Gathered B rows give exactly the wgrad over the materialised rows (same accumulation order)."""
+    import os
+    tpe = make_tpe("ragged", m + nb, m, e)
+    g = torch.from_numpy(synth.normal(m + 5, (m, na))).to(dtype).to(cuda)
+    b = torch.from_numpy(synth.normal(m + 6, (b_rows, nb))).to(dtype).to(cuda)
+    idx = torch.from_numpy(np.random.default_rng(m).integers(0, b_rows, size=m)).to(torch.int32).to(cuda)
+    tpe_d = torch.from_numpy(tpe).to(cuda)
+    old = os.environ.get("HRM_MOE_WGRAD_STAGES")
+    os.environ["HRM_MOE_WGRAD_STAGES"] = kernel
+    try:
+        got = ops.grouped_gemm_tn_gather(g, b, idx, tpe_d)
+        want = ops.grouped_gemm_tn(g, b.index_select(0, idx.long()), tpe_d)
+    finally:
+        if old is None:
+            os.environ.pop("HRM_MOE_WGRAD_STAGES", None)
+        else:
+            os.environ["HRM_MOE_WGRAD_STAGES"] = old
+    assert torch.equal(got, want)
+    ref = mo.grouped_linear_wgrad(g.cpu(), b.cpu().index_select(0, idx.cpu().long()), tpe, num_experts=e)
+    close(got, ref, f"tn_gather {m}x{na}x{nb} e{e}")
+
+
 def test_grouped_linear_autograd_matches_oracle(cuda):
     m, n, k, e = 3000, 512, 384, 16
     tpe = ragged_tpe(77, m, e)
