@@ -585,11 +585,13 @@ __device__ __forceinline__ float swiglu_fast(float g, float u) {
 // points (torch autograd on 16-bit tensors): the saved silu output is rounded,
 // d_up = da * silu(g) and d_silu = da * u are rounded products, and silu's
 // backward is computed in fp32 as d_silu * sig * (1 + g * (1 - sig)) and rounded.
+// sig = 1 / (1 + e^-g) uses the hardware exp2 and reciprocal, as the forward's
+// swiglu_fast does: an exact expf and two IEEE divisions made this epilogue
+// cost more VALU time per tile than the tile's MFMAs.
 template <typename TR>
 __device__ __forceinline__ void swiglu_bwd(float da, float g, float u, float& dg, float& du) {
-  const float den = 1.0f + expf(-g);
-  const float sig = 1.0f / den;
-  const float sl = TR::to_f(TR::from_f(g / den));
+  const float sig = __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-g * 1.4426950408889634f));
+  const float sl = TR::to_f(TR::from_f(g * sig));
   du = TR::to_f(TR::from_f(da * sl));
   const float ds = TR::to_f(TR::from_f(da * u));
   dg = TR::to_f(TR::from_f(ds * sig * (1.0f + g * (1.0f - sig))));
@@ -966,8 +968,20 @@ __global__ __launch_bounds__(NW * 64, NW == 4 ? 2 : 1) void mgemm_dma_kernel(con
               *reinterpret_cast<u32x2*>(stg + r * PITCH + ((ch8 ^ g) << 3)) = pack4<TR>(o[0], o[1], o[2], o[3]);
             }
         }
+        constexpr int ITER = APP * 32 / RPI;  // read-back rows per lane in this pass
+        // EPI_SWIGLU_BWD: byte offset of the gate values of read-back i's row and columns
+        auto xoff_of = [&](int i) __attribute__((always_inline)) -> uint32_t {
+          const uint32_t ml = (uint32_t)(row_base + a0 * 32 + i * RPI + lane / LPR);
+          const int c = col0 + (lane % LPR) * 8;
+          return c < N ? (ml * (uint32_t)N * 2 + (uint32_t)c) * 2 : 0x80000000u;
+        };
+        u32x4 g_next = u32x4{0u, 0u, 0u, 0u}, u_next = g_next;
+        if constexpr (EPI == EPI_SWIGLU_BWD) {  // first row's gate/up, in flight during the staging reads
+          g_next = bload16(rX, xoff_of(0));
+          u_next = bload16(rX, xoff_of(0) + (uint32_t)N * 2);
+        }
 #pragma unroll
-        for (int i = 0; i < APP * 32 / RPI; ++i) {
+        for (int i = 0; i < ITER; ++i) {
           const int r = i * RPI + lane / LPR;
           const int c16 = lane % LPR;
           const int g = (r / RP) % C8;
@@ -976,9 +990,14 @@ __global__ __launch_bounds__(NW * 64, NW == 4 ? 2 : 1) void mgemm_dma_kernel(con
           const uint32_t ml = (uint32_t)(row_base + a0 * 32 + r);
           const int c = col0 + c16 * 8;
           if constexpr (EPI == EPI_SWIGLU_BWD) {
-            // v holds dAct (rounded); gate and up of the same elements come from aux
-            const uint32_t xoff = c < N ? (ml * (uint32_t)N * 2 + (uint32_t)c) * 2 : 0x80000000u;
-            const u32x4 gv = bload16(rX, xoff), uv = bload16(rX, xoff + (uint32_t)N * 2);
+            // v holds dAct (rounded); gate and up of the same elements come from aux,
+            // loaded one read-back ahead
+            const uint32_t xoff = xoff_of(i);
+            const u32x4 gv = g_next, uv = u_next;
+            if (i + 1 < ITER) {
+              g_next = bload16(rX, xoff_of(i + 1));
+              u_next = bload16(rX, xoff_of(i + 1) + (uint32_t)N * 2);
+            }
             u32x4 dgv, duv;
 #pragma unroll
             for (int h2 = 0; h2 < 4; ++h2) {
