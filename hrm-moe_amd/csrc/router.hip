@@ -263,6 +263,61 @@ int launch_router_np2(const void* logits, int ldt, int64_t T, int E, int k, int 
   return HRM_MOE_OK;
 }
 
+// Backward of the router (models/layers.py:606-610) as torch autograd computes it:
+//   v_j = p[idx_j],  s = sum_j v_j,  c = max(s, 1e-12)
+//   dv_j = g_w[j] / c - (sum_i g_w[i] v_i) / c^2 * [s >= 1e-12]   (norm_topk_prob; else dv_j = g_w[j])
+//   dp_e = g_probs[e] + sum_{j: idx_j = e} dv_j                   (topk backward scatters to the chosen experts)
+//   dlogits_e = p_e * (dp_e - sum_e' p_e' dp_e')                  (softmax backward)
+// One wave per token; lane l holds experts l and l + 64.  The two sums over a
+// row are fixed xor butterflies, so results are deterministic.
+constexpr int kBwdTokPerBlock = 4;
+__global__ __launch_bounds__(kBwdTokPerBlock * 64) void router_bwd_kernel(
+    const float* __restrict__ probs, const int64_t* __restrict__ idx, const void* __restrict__ g_w, int gw_dt,
+    const float* __restrict__ g_probs, int64_t T, int E, int k, int norm, void* __restrict__ dlogits, int out_dt) {
+  const int lane = threadIdx.x & 63;
+  const int64_t t = (int64_t)blockIdx.x * kBwdTokPerBlock + (threadIdx.x >> 6);
+  if (t >= T) return;  // no barriers below
+  auto wsum = [](float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    return v;
+  };
+  const float* prow = probs + t * E;
+  int ej = -1;
+  float gj = 0.0f, vj = 0.0f;
+  if (lane < k) {
+    ej = (int)idx[t * k + lane];
+    gj = load_logit(g_w, gw_dt, t * k + lane);
+    vj = (ej >= 0 && ej < E) ? prow[ej] : 0.0f;
+  }
+  float dv = gj;
+  if (norm) {
+    const float sum = wsum(vj);
+    const float dot = wsum(gj * vj);
+    const float c = fmaxf(sum, 1e-12f);
+    dv = gj / c - (sum >= 1e-12f ? dot / (c * c) : 0.0f);
+  }
+  float p[2], dp[2];
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const int e = lane + 64 * h;
+    p[h] = e < E ? prow[e] : 0.0f;
+    dp[h] = (e < E && g_probs) ? g_probs[t * E + e] : 0.0f;
+  }
+  for (int j = 0; j < k; ++j) {
+    const int e = __shfl(ej, j, 64);
+    const float d = __shfl(dv, j, 64);
+#pragma unroll
+    for (int h = 0; h < 2; ++h) dp[h] += (lane + 64 * h == e) ? d : 0.0f;
+  }
+  const float pd = wsum(p[0] * dp[0] + p[1] * dp[1]);
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const int e = lane + 64 * h;
+    if (e < E) store_weight(dlogits, out_dt, t * E + e, p[h] * (dp[h] - pd));
+  }
+}
+
 }  // namespace
 }  // namespace hrm
 
@@ -279,4 +334,22 @@ extern "C" int hrm_moe_router_topk(const void* logits, int logits_dtype, int64_t
   if (E <= 8) return hrm::launch_router_np2<8, 4>(logits, logits_dtype, num_tokens, E, k, norm_topk_prob, probs, topk_idx, topk_weight, weight_dtype, stream);
   if (E <= 64) return hrm::launch_router_np2<64, 4>(logits, logits_dtype, num_tokens, E, k, norm_topk_prob, probs, topk_idx, topk_weight, weight_dtype, stream);
   return hrm::launch_router_np2<128, 4>(logits, logits_dtype, num_tokens, E, k, norm_topk_prob, probs, topk_idx, topk_weight, weight_dtype, stream);
+}
+
+extern "C" int hrm_moe_router_topk_backward(const float* probs, const int64_t* topk_idx, const void* grad_weight,
+                                            int grad_weight_dtype, const float* grad_probs, int64_t num_tokens,
+                                            int32_t num_experts, int32_t top_k, int32_t norm_topk_prob,
+                                            void* grad_logits, int logits_dtype, void* stream) {
+  if (num_tokens < 0 || num_experts < 1 || top_k < 1 || top_k > num_experts) return HRM_MOE_ERR_INVALID;
+  if (grad_weight_dtype < HRM_MOE_BF16 || grad_weight_dtype > HRM_MOE_F32) return HRM_MOE_ERR_DTYPE;
+  if (logits_dtype < HRM_MOE_BF16 || logits_dtype > HRM_MOE_F32) return HRM_MOE_ERR_DTYPE;
+  if (num_experts > 128 || top_k > 32) return HRM_MOE_ERR_UNSUPPORTED;
+  if (num_tokens == 0) return HRM_MOE_OK;
+  if (!probs || !topk_idx || !grad_weight || !grad_logits) return HRM_MOE_ERR_INVALID;
+  const dim3 grid((unsigned)((num_tokens + hrm::kBwdTokPerBlock - 1) / hrm::kBwdTokPerBlock));
+  hipLaunchKernelGGL(hrm::router_bwd_kernel, grid, dim3(hrm::kBwdTokPerBlock * 64), 0, (hipStream_t)stream, probs,
+                     topk_idx, grad_weight, grad_weight_dtype, grad_probs, num_tokens, num_experts, top_k,
+                     norm_topk_prob, grad_logits, logits_dtype);
+  const hipError_t err = hipGetLastError();
+  return err == hipSuccess ? HRM_MOE_OK : (int)err;
 }

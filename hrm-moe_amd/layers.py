@@ -76,8 +76,7 @@ def load_balancing_loss_func(routing_weights: Tensor, selected_experts: Tensor, 
 class _RouterTopK(torch.autograd.Function):
     """Router kernel with the gradient of softmax -> top-k gather -> renormalise -> cast.
 
-    Forward is one HIP launch (models/layers.py:606-610).  Backward is the
-    chain rule of those ops, in torch ops on the device:
+    Forward and backward are one HIP launch each (models/layers.py:606-610):
       dv  = dw / c - <dw, v> / c^2 * [s >= 1e-12],  c = max(s, 1e-12), s = sum(v)
       dp  = dprobs + scatter(idx, dv)
       dz  = p * (dp - <p, dp>)
@@ -95,19 +94,11 @@ class _RouterTopK(torch.autograd.Function):
     @staticmethod
     def backward(ctx, g_probs, g_w, _g_idx):
         probs, idx = ctx.saved_tensors
-        dp = torch.zeros_like(probs) if g_probs is None else g_probs.float().clone()
-        if g_w is not None:
-            v = probs.gather(1, idx)
-            gw = g_w.float()
-            if ctx.norm:
-                s = v.sum(dim=-1, keepdim=True)
-                c = s.clamp_min(1e-12)
-                dv = gw / c - (gw * v).sum(dim=-1, keepdim=True) / (c * c) * (s >= 1e-12).float()
-            else:
-                dv = gw
-            dp.scatter_add_(1, idx, dv)
-        dz = probs * (dp - (probs * dp).sum(dim=-1, keepdim=True))
-        return dz.to(ctx.logits_dtype), None, None, None
+        if g_w is None:
+            g_w = torch.zeros(idx.shape, dtype=torch.float32, device=probs.device)
+        g_probs = None if g_probs is None else g_probs.float()
+        dz = ops.router_topk_backward(probs, idx, g_w, g_probs, ctx.norm, ctx.logits_dtype)
+        return dz, None, None, None
 
 
 class _GroupedExpertsFn(torch.autograd.Function):

@@ -57,6 +57,29 @@ def router_topk(logits: torch.Tensor, top_k: int, norm_topk_prob: bool, weight_d
     return probs, w, idx
 
 
+def router_topk_backward(probs: torch.Tensor, topk_idx: torch.Tensor, grad_weight: torch.Tensor,
+                         grad_probs: Optional[torch.Tensor], norm_topk_prob: bool,
+                         logits_dtype: torch.dtype) -> torch.Tensor:
+    """d logits [T,E] of router_topk, from the grads of its weights [T,k] and (optionally) probs [T,E]."""
+    dev = _require_cuda(probs, topk_idx, grad_weight, grad_probs)
+    t, e = probs.shape
+    k = topk_idx.shape[1]
+    if probs.dtype != torch.float32 or (grad_probs is not None and grad_probs.dtype != torch.float32):
+        raise TypeError("router backward needs fp32 probabilities and probability grads")
+    probs = probs.contiguous()
+    topk_idx = topk_idx.to(torch.int64).contiguous()
+    grad_weight = grad_weight.contiguous()
+    grad_probs = grad_probs.contiguous() if grad_probs is not None else None
+    out = torch.empty((t, e), dtype=logits_dtype, device=dev)
+    with _lib.device_guard(dev):
+        st = _lib.lib().hrm_moe_router_topk_backward(
+            _lib.ptr(probs), _lib.ptr(topk_idx), _lib.ptr(grad_weight), _lib.dtype_code(grad_weight.dtype),
+            _lib.ptr(grad_probs), t, e, k, int(bool(norm_topk_prob)), _lib.ptr(out), _lib.dtype_code(logits_dtype),
+            _lib.stream_of(dev))
+    _lib.check(st, "router_topk_backward")
+    return out
+
+
 # ---------------------------------------------------------------------------
 # Dispatch (models/layers.py:312-322)
 # ---------------------------------------------------------------------------

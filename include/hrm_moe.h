@@ -190,6 +190,20 @@ int hrm_moe_combine_backward(const void* grad_out, const void* expert_out, const
                              int32_t top_k, int64_t hidden_size, int32_t num_experts, int dtype,
                              void* grad_expert_out, void* grad_weight, void* stream);
 
+/* Backward of hrm_moe_router_topk (models/layers.py:606-610 under autograd):
+ *   v_j = probs[t, idx_j], s = sum_j v_j, c = max(s, 1e-12)
+ *   dv_j = g_w[t,j] / c - (sum_i g_w[t,i] v_i) / c^2 * [s >= 1e-12]   (norm_topk_prob; else dv_j = g_w[t,j])
+ *   dp[t,e] = grad_probs[t,e] + sum over j with idx_j = e of dv_j
+ *   grad_logits[t,e] = probs[t,e] * (dp[t,e] - sum_e' probs[t,e'] dp[t,e'])
+ * probs [T,E] fp32 (the forward's output), topk_idx [T,k] int64, grad_weight
+ * [T,k], grad_probs [T,E] fp32 or NULL (no gradient reaches the
+ * probabilities), grad_logits [T,E] in logits_dtype.  Deterministic.
+ * Limits: E <= 128, k <= 32. */
+int hrm_moe_router_topk_backward(const float* probs, const int64_t* topk_idx, const void* grad_weight,
+                                 int grad_weight_dtype, const float* grad_probs, int64_t num_tokens,
+                                 int32_t num_experts, int32_t top_k, int32_t norm_topk_prob, void* grad_logits,
+                                 int logits_dtype, void* stream);
+
 /* hrm_moe_grouped_gemm_tn with the B operand's rows gathered:
  *   C[e][Na,Nb] = A[rows_e]^T . B[b_row_index[rows_e]]
  * with B [b_rows, Nb] and b_row_index [M] (values in [0, b_rows); others read

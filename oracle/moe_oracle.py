@@ -24,7 +24,9 @@ Pinning (what checks each function; tests/test_oracle.py):
                   (models/layers.py:481-515) computed independently.
   experts_vjp     float64 gradients equal those of the independent per-expert
                   formulation and a central finite difference along a random
-                  direction.
+                  direction; with router_vjp and the aux loss it reproduces the
+                  C1 golden's gate-weight and hidden-state gradients.
+  router_vjp      the same C1 golden chain; float64 finite differences.
   aux_loss        closed form vs C1 golden.
 """
 from __future__ import annotations
@@ -321,6 +323,28 @@ def moe_forward_origin(x: torch.Tensor, gate_weight: torch.Tensor, gate_up_weigh
         y = ((F.silu(gate) * up).float() @ down_weight[e].float().T).to(h.dtype)
         out.index_add_(0, tok, (y * w[tok, slot, None]).to(h.dtype))
     return out.reshape(shape)
+
+
+def router_vjp(logits: torch.Tensor, norm_topk_prob: bool, idx, g_weights: torch.Tensor,
+               g_probs: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """d logits of softmax(fp32) -> top-k gather -> renormalise (models/layers.py:606-609) by CPU autograd.
+
+    torch.topk's backward scatters the value grads to the selected experts,
+    which is what gathering the probabilities at ``idx`` differentiates to.
+    ``g_probs`` is the gradient reaching the probabilities directly (the aux
+    loss, :619-627).  Returned in the logits' dtype, as softmax(dtype=float32)
+    hands its gradient back.
+    """
+    z = logits.detach().clone().requires_grad_(True)
+    p = F.softmax(z, dim=-1, dtype=torch.float32)
+    v = p.gather(1, torch.as_tensor(np.asarray(idx), dtype=torch.int64))
+    w = v / v.sum(dim=-1, keepdim=True).clamp_min(1e-12) if norm_topk_prob else v
+    outs, grads = [w], [g_weights.float()]
+    if g_probs is not None:
+        outs.append(p)
+        grads.append(g_probs.float())
+    torch.autograd.backward(outs, grads)
+    return z.grad
 
 
 def experts_vjp(h: torch.Tensor, w: torch.Tensor, gate_up_weight: torch.Tensor, down_weight: torch.Tensor,

@@ -105,6 +105,12 @@ def test_training_entry_points_reject_bad_arguments():
     assert d(buf, buf, buf, buf, 128, 60, 256, 64, _lib.BF16, buf, buf, ws, NULL) == _lib.ERR_UNSUPPORTED
     assert d(buf, buf, buf, NULL, 128, 64, 256, 64, _lib.BF16, buf, buf, ws, NULL) == _lib.ERR_INVALID
     assert d(buf, buf, buf, buf, 0, 64, 256, 64, _lib.BF16, buf, buf, ws, NULL) == _lib.OK
+    rb = lib.hrm_moe_router_topk_backward
+    assert rb(buf, buf, buf, _lib.BF16, NULL, 16, 200, 8, 1, buf, _lib.BF16, NULL) == _lib.ERR_UNSUPPORTED
+    assert rb(buf, buf, buf, 9, NULL, 16, 64, 8, 1, buf, _lib.BF16, NULL) == _lib.ERR_DTYPE
+    assert rb(buf, buf, buf, _lib.BF16, NULL, 16, 64, 65, 1, buf, _lib.BF16, NULL) == _lib.ERR_INVALID
+    assert rb(buf, NULL, buf, _lib.BF16, NULL, 16, 64, 8, 1, buf, _lib.BF16, NULL) == _lib.ERR_INVALID
+    assert rb(buf, buf, buf, _lib.BF16, NULL, 0, 64, 8, 1, buf, _lib.BF16, NULL) == _lib.OK
     tg = lib.hrm_moe_grouped_gemm_tn_gather
     assert tg(buf, buf, buf, 100, buf, 1024, 256, 252, 64, _lib.BF16, buf, buf, ws, NULL) == _lib.ERR_UNSUPPORTED
     assert tg(buf, buf, NULL, 100, buf, 1024, 256, 256, 64, _lib.BF16, buf, buf, ws, NULL) == _lib.ERR_INVALID

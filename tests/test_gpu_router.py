@@ -97,3 +97,28 @@ def test_router_without_probs_output(cuda):
 def test_router_zero_tokens(cuda):
     probs, w, idx = ops.router_topk(torch.empty(0, 64, device=cuda, dtype=torch.bfloat16), 8, True, torch.bfloat16)
     assert idx.shape == (0, 8) and w.shape == (0, 8)
+
+
+@pytest.mark.parametrize("t,e,k,norm,with_gp", [
+    (300, 8, 2, True, True), (1000, 64, 8, True, True), (513, 128, 8, True, False),
+    (257, 64, 4, False, True), (64, 16, 16, True, True),
+])
+def test_router_backward_matches_oracle(cuda, t, e, k, norm, with_gp):
+    """d logits of the router kernel vs CPU autograd of softmax -> gather -> renormalise (oracle.router_vjp)."""
+    from oracle import moe_oracle as mo
+    from oracle import synth
+    logits = torch.from_numpy(synth.normal(t + e, (t, e))).to(torch.bfloat16)
+    probs, _, idx = ops.router_topk(logits.to(cuda), k, norm, torch.bfloat16)
+    gw = torch.from_numpy(synth.normal(t + 1, (t, k))).to(torch.bfloat16)
+    gp = torch.from_numpy(synth.normal(t + 2, (t, e), std=0.1)) if with_gp else None
+    got = ops.router_topk_backward(probs, idx, gw.to(cuda), gp.to(cuda) if gp is not None else None, norm,
+                                   torch.bfloat16)
+    ref = mo.router_vjp(logits, norm, idx.cpu().numpy(), gw, gp)
+    assert got.dtype == torch.bfloat16 and got.shape == (t, e)
+    d = (got.float().cpu() - ref.float()).abs()
+    rel = d.max().item() / ref.float().abs().max().item()
+    print(f"router backward E={e} k={k}: max rel err {rel:.3e}, mean abs err {d.mean().item():.3e}")
+    assert rel <= 1e-2
+    again = ops.router_topk_backward(probs, idx, gw.to(cuda), gp.to(cuda) if gp is not None else None, norm,
+                                     torch.bfloat16)
+    assert torch.equal(got, again)

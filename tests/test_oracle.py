@@ -352,3 +352,45 @@ def test_experts_vjp_planted_wrong_swiglu_grad_is_caught():
     swapped = torch.cat([wgu[:, i:], wgu[:, :i]], dim=1)
     r2 = mo.experts_vjp(x, w, swapped, wdn, idx, g)
     assert not torch.allclose(r["d_hidden"], r2["d_hidden"], atol=1e-6)
+
+
+def test_training_chain_reproduces_c1_golden_router_and_input_grads(c1):
+    """experts_vjp + router_vjp + the aux loss give the reference module's gate and input gradients."""
+    (x, wg, wgu, wdn), k, e = _c1_inputs(c1)
+    t, h = x.shape
+    grad = torch.from_numpy(synth.normal(12, (t, h)))
+    logits = F.linear(x, wg)
+    probs, w, idx = mo.router_topk(logits, k, True, x.dtype)
+    r = mo.experts_vjp(x, w, wgu, wdn, idx.numpy(), grad)
+    p = probs.detach().clone().requires_grad_(True)
+    mo.load_balancing_loss(p, idx, e).backward()
+    dlogits = mo.router_vjp(logits, True, idx.numpy(), r["d_weights"], p.grad)
+    gate_grad = dlogits.T @ x
+    x_grad = r["d_hidden"] + dlogits @ wg
+    assert torch.allclose(gate_grad, torch.from_numpy(c1["c1_grouped_triton__gate_grad"]), rtol=1e-4, atol=1e-6)
+    assert torch.allclose(x_grad[:16], torch.from_numpy(c1["c1_grouped_triton__x_grad_rows0_15"]), rtol=1e-4,
+                          atol=1e-6)
+    sq = float(x_grad.double().pow(2).sum())
+    assert abs(sq / float(c1["c1_grouped_triton__x_grad_sq_sum"]) - 1.0) < 1e-5
+
+
+def test_router_vjp_finite_differences():
+    t, e, k = 12, 10, 3
+    rng = np.random.default_rng(3)
+    z = torch.from_numpy(rng.standard_normal((t, e)))
+    idx = torch.topk(F.softmax(z, -1), k).indices
+    gw = torch.from_numpy(rng.standard_normal((t, k)))
+    gp = torch.from_numpy(rng.standard_normal((t, e)))
+    v = torch.from_numpy(rng.standard_normal((t, e)))
+    for norm in (True, False):
+        dz = mo.router_vjp(z, norm, idx.numpy(), gw, gp)
+
+        def f(s):
+            p = F.softmax(z + s * v, dim=-1, dtype=torch.float64)
+            sel = p.gather(1, idx)
+            w = sel / sel.sum(-1, keepdim=True) if norm else sel
+            return float((w * gw).sum() + (p * gp).sum())
+
+        eps = 1e-6
+        fd = (f(eps) - f(-eps)) / (2 * eps)
+        assert abs(fd - float((dz * v).sum())) < 1e-6
