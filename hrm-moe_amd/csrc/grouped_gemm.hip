@@ -518,6 +518,24 @@ __global__ __launch_bounds__(kThreads, 1) void wgrad_kernel(const uint16_t* __re
   }
 }
 
+// Row counts of S equal splits of T rows (the first T % S splits one longer),
+// the "experts" of the split-K router gate weight gradient.
+__global__ void split_rows_kernel(int64_t* __restrict__ tpe, int S, int64_t T) {
+  const int s = blockIdx.x * blockDim.x + threadIdx.x;
+  if (s < S) tpe[s] = T / S + (s < T % S ? 1 : 0);
+}
+
+// out[i] = round(sum_s part[s][i]) over the S partials in split order (deterministic).
+template <typename TR>
+__global__ __launch_bounds__(256) void sum_splits_kernel(const float* __restrict__ part, int S, int64_t n,
+                                                         uint16_t* __restrict__ out) {
+  const int64_t i = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 4;
+  if (i >= n) return;
+  floatx4 acc = floatx4{0.f, 0.f, 0.f, 0.f};
+  for (int s = 0; s < S; ++s) acc += *reinterpret_cast<const floatx4*>(part + (int64_t)s * n + i);
+  st8(out + i, pack4<TR>(acc[0], acc[1], acc[2], acc[3]));
+}
+
 // ---------------------------------------------------------------------------
 // DMA-fed kernels: buffer_load ... lds fills a ring of LDS stages directly
 // ---------------------------------------------------------------------------
@@ -1355,8 +1373,9 @@ __global__ __launch_bounds__(NW * 64, 1) void wgrad_dma8_kernel(const uint16_t* 
 
 // Wgrad fed by DMA: both operands are [64 rows][128 cols] tiles of the
 // expert's rows; rows past the expert's end read as zeros (buffer bounds).
-// GB: gathered B rows, as in wgrad_dma8_kernel.
-template <typename TR, int STAGES, bool GB = false>
+// GB: gathered B rows, as in wgrad_dma8_kernel.  F32OUT: C is fp32 (the
+// per-split partial sums of the router gate's weight gradient).
+template <typename TR, int STAGES, bool GB = false, bool F32OUT = false>
 __global__ __launch_bounds__(kThreads, 1) void wgrad_dma_kernel(const uint16_t* __restrict__ A,
                                                                const uint16_t* __restrict__ B,
                                                                uint16_t* __restrict__ C,
@@ -1467,6 +1486,7 @@ __global__ __launch_bounds__(kThreads, 1) void wgrad_dma_kernel(const uint16_t* 
     barrier_lds();
 
     uint16_t* Ce = C + (int64_t)e * Na * Nb;
+    float* Cf = reinterpret_cast<float*>(C) + (int64_t)e * Na * Nb;
 #pragma unroll
     for (int a = 0; a < MB; ++a) {
       const int na = a0 + wa * (BA / 2) + a * 32 + (lane & 31);
@@ -1476,7 +1496,11 @@ __global__ __launch_bounds__(kThreads, 1) void wgrad_dma_kernel(const uint16_t* 
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
           const int nb = b0 + wb * (BB / 2) + b * 32 + g * 8 + (lane >> 5) * 4;
-          if (nb < Nb)
+          if (nb >= Nb) continue;
+          if constexpr (F32OUT)
+            *reinterpret_cast<floatx4*>(Cf + (int64_t)na * Nb + nb) =
+                floatx4{acc[b][a][g * 4 + 0], acc[b][a][g * 4 + 1], acc[b][a][g * 4 + 2], acc[b][a][g * 4 + 3]};
+          else
             st8(Ce + (int64_t)na * Nb + nb, pack4<TR>(acc[b][a][g * 4 + 0], acc[b][a][g * 4 + 1],
                                                      acc[b][a][g * 4 + 2], acc[b][a][g * 4 + 3]));
         }
@@ -1754,8 +1778,80 @@ int launch_wgrad(const void* A, const void* B, const int64_t* tpe, int64_t M, in
   return HRM_MOE_OK;
 }
 
+// Router gate weight gradient dW[E,H] = dlogits[T,E]^T . h[T,H]: a wgrad over
+// S row splits with fp32 partials, then one ordered sum.  One long reduction
+// (T rows) into a small output is what library GEMMs tile poorly.
+// Rows per split: HRM_MOE_GATE_SPLIT_ROWS (default 1024).  At T = 16384,
+// E = 64, H = 1280: 256 / 512 / 1024 / 2048 rows measured 50 / 37 / 36 / 47 us
+// (torch's matmul: 101 us); short splits are dominated by each tile's pipeline
+// fill and epilogue, long ones leave CUs idle.
+inline int gate_wgrad_splits(int64_t T) {
+  static const int64_t rows = [] {
+    const char* env = getenv("HRM_MOE_GATE_SPLIT_ROWS");
+    const int64_t v = env ? atoll(env) : 1024;
+    return v < 64 ? int64_t(64) : v;
+  }();
+  int64_t s = T / rows;
+  return (int)(s < 1 ? 1 : (s > 128 ? 128 : s));
+}
+inline size_t gate_wgrad_ws_bytes(int64_t T, int E, int64_t H) {
+  const int S = gate_wgrad_splits(T);
+  return align256(sizeof(int64_t) * S) + align256(gemm_ws_bytes(T, S, kBMMin)) + align256(sizeof(float) * S * E * H);
+}
+
+template <typename TR>
+int launch_gate_wgrad(const void* dlogits, const void* hidden, int64_t T, int E, int H, void* out, void* ws,
+                      void* stream) {
+  const int S = gate_wgrad_splits(T);
+  char* p = static_cast<char*>(ws);
+  int64_t* tpe = reinterpret_cast<int64_t*>(p);
+  p += align256(sizeof(int64_t) * S);
+  void* gws = p;
+  p += align256(gemm_ws_bytes(T, S, kBMMin));
+  float* part = reinterpret_cast<float*>(p);
+  HRM_LAUNCH(split_rows_kernel, dim3((S + 255) / 256), dim3(256), 0, stream, tpe, S, T);
+  GemmWs w = carve(gws, T, S, kBMMin);
+  const int max_tiles = (int)((T + kBMMin - 1) / kBMMin + S);
+  HRM_LAUNCH(plan_kernel, dim3(1), dim3(1024), 0, stream, tpe, S, T, kBMMin, w.tiles, max_tiles, w.count,
+             w.row_offsets, w.work_counter);
+  auto kern = wgrad_dma_kernel<TR, 2, false, true>;
+  static int grid = 0;
+  if (grid == 0) grid = persistent_grid(kern);
+  HRM_LAUNCH(kern, dim3(grid), dim3(kThreads), 0, stream, (const uint16_t*)dlogits, (const uint16_t*)hidden,
+             (uint16_t*)part, w.row_offsets, S, E, H, w.work_counter, nullptr, 0u);
+  const int64_t n = (int64_t)E * H;
+  HRM_LAUNCH(sum_splits_kernel<TR>, dim3((unsigned)((n / 4 + 255) / 256)), dim3(256), 0, stream, part, S, n,
+             (uint16_t*)out);
+  return HRM_MOE_OK;
+}
+
 }  // namespace
 }  // namespace hrm
+
+extern "C" size_t hrm_moe_gate_wgrad_workspace_size(int64_t num_tokens, int32_t num_experts, int64_t hidden_size) {
+  if (num_tokens < 0 || num_experts < 1 || hidden_size < 1) return 0;
+  return hrm::gate_wgrad_ws_bytes(num_tokens, num_experts, hidden_size);
+}
+
+extern "C" int hrm_moe_gate_wgrad(const void* grad_logits, const void* hidden, int64_t num_tokens, int32_t num_experts,
+                                  int64_t hidden_size, int dtype, void* grad_gate_weight, void* workspace,
+                                  size_t workspace_bytes, void* stream) {
+  if (num_tokens < 0 || num_experts < 1 || hidden_size < 1) return HRM_MOE_ERR_INVALID;
+  if (dtype != HRM_MOE_BF16 && dtype != HRM_MOE_F16) return HRM_MOE_ERR_DTYPE;
+  if (num_experts % 8 || hidden_size % 8 || num_experts >= (1 << 20) || hidden_size >= (1 << 30) ||
+      num_tokens >= (int64_t(1) << 31) || num_tokens * hidden_size * 2 >= (int64_t(1) << 32) ||
+      num_tokens * (int64_t)num_experts * 2 >= (int64_t(1) << 32))
+    return HRM_MOE_ERR_UNSUPPORTED;
+  if (!workspace || workspace_bytes < hrm::gate_wgrad_ws_bytes(num_tokens, num_experts, hidden_size))
+    return HRM_MOE_ERR_WORKSPACE;
+  if (!grad_logits || !hidden || !grad_gate_weight) return HRM_MOE_ERR_INVALID;
+  if (num_tokens == 0) return HRM_MOE_ERR_INVALID;
+  if (dtype == HRM_MOE_BF16)
+    return hrm::launch_gate_wgrad<hrm::BF16>(grad_logits, hidden, num_tokens, num_experts, (int)hidden_size,
+                                            grad_gate_weight, workspace, stream);
+  return hrm::launch_gate_wgrad<hrm::F16>(grad_logits, hidden, num_tokens, num_experts, (int)hidden_size,
+                                         grad_gate_weight, workspace, stream);
+}
 
 extern "C" size_t hrm_moe_grouped_gemm_workspace_size(int64_t num_rows, int32_t num_experts) {
   if (num_rows < 0 || num_experts < 1 || num_experts > hrm::kMaxExperts) return 0;

@@ -73,6 +73,31 @@ def load_balancing_loss_func(routing_weights: Tensor, selected_experts: Tensor, 
     return torch.sum(tokens_per_expert * router_prob_per_expert) * num_experts
 
 
+class _GateLinear(torch.autograd.Function):
+    """The router gate ``F.linear(h, W)`` (models/layers.py:605, :89-90) with a HIP weight gradient.
+
+    Forward is the same F.linear call, so the logits are the same bits.  The
+    backward's input grad is ``dlogits @ W``; the weight grad ``dlogits^T @ h``
+    (one long reduction over the tokens into a small [E,H] output) runs as a
+    split-K HIP kernel with fp32 partials.
+    """
+
+    @staticmethod
+    def forward(ctx, hidden: Tensor, weight: Tensor):
+        ctx.save_for_backward(hidden, weight)
+        return F.linear(hidden, weight)
+
+    @staticmethod
+    def backward(ctx, grad_logits: Tensor):
+        hidden, weight = ctx.saved_tensors
+        grad_logits = grad_logits.to(hidden.dtype)
+        d_hidden = grad_logits @ weight if ctx.needs_input_grad[0] else None
+        d_weight = None
+        if ctx.needs_input_grad[1]:
+            d_weight = ops.gate_wgrad(grad_logits, hidden).to(weight.dtype)
+        return d_hidden, d_weight
+
+
 class _RouterTopK(torch.autograd.Function):
     """Router kernel with the gradient of softmax -> top-k gather -> renormalise -> cast.
 
@@ -285,7 +310,14 @@ class SparseMoESwiGLU(nn.Module):
         want_aux = moe_context is not None and torch.is_grad_enabled()
 
         with record_moe_profile_phase("router"):
-            router_logits = self.gate(hidden_states)
+            w_gate = self.gate.weight
+            if (torch.is_grad_enabled() and w_gate.requires_grad and self.gate.bias is None
+                    and hidden_states.dtype == w_gate.dtype
+                    and hidden_states.dtype in (torch.bfloat16, torch.float16) and self.num_experts % 8 == 0
+                    and self.hidden_size % 8 == 0):
+                router_logits = _GateLinear.apply(hidden_states, w_gate)
+            else:
+                router_logits = self.gate(hidden_states)
             if torch.is_grad_enabled() and router_logits.requires_grad:
                 routing_probs, routing_weights, selected_experts = _RouterTopK.apply(
                     router_logits, self.top_k, self.norm_topk_prob, hidden_states.dtype)

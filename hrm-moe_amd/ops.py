@@ -57,6 +57,27 @@ def router_topk(logits: torch.Tensor, top_k: int, norm_topk_prob: bool, weight_d
     return probs, w, idx
 
 
+def gate_wgrad(grad_logits: torch.Tensor, hidden: torch.Tensor) -> torch.Tensor:
+    """grad of the gate weight [E,H] = grad_logits[T,E]^T @ hidden[T,H] (split-K, fp32 partials, one rounding)."""
+    dev = _require_cuda(grad_logits, hidden)
+    t, e = grad_logits.shape
+    th, h = hidden.shape
+    if th != t:
+        raise ValueError(f"gate wgrad: {t} logit rows for {th} hidden rows")
+    if grad_logits.dtype != hidden.dtype:
+        raise TypeError(f"gate wgrad dtype mismatch: {grad_logits.dtype} vs {hidden.dtype}")
+    dt = _gemm_dtype(hidden)
+    grad_logits, hidden = grad_logits.contiguous(), hidden.contiguous()
+    out = hidden.new_empty((e, h))
+    lib = _lib.lib()
+    ws = _workspace(lib.hrm_moe_gate_wgrad_workspace_size(t, e, h), dev)
+    with _lib.device_guard(dev):
+        st = lib.hrm_moe_gate_wgrad(_lib.ptr(grad_logits), _lib.ptr(hidden), t, e, h, dt, _lib.ptr(out),
+                                    _lib.ptr(ws), ws.numel(), _lib.stream_of(dev))
+    _lib.check(st, "gate_wgrad")
+    return out
+
+
 def router_topk_backward(probs: torch.Tensor, topk_idx: torch.Tensor, grad_weight: torch.Tensor,
                          grad_probs: Optional[torch.Tensor], norm_topk_prob: bool,
                          logits_dtype: torch.dtype) -> torch.Tensor:

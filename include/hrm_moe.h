@@ -204,6 +204,17 @@ int hrm_moe_router_topk_backward(const float* probs, const int64_t* topk_idx, co
                                  int32_t num_experts, int32_t top_k, int32_t norm_topk_prob, void* grad_logits,
                                  int logits_dtype, void* stream);
 
+/* Router gate weight gradient: grad_gate_weight[E,H] = grad_logits[T,E]^T . hidden[T,H],
+ * the weight grad of F.linear(hidden, gate.weight) (models/layers.py:605, :89-90)
+ * that torch autograd computes.  The T rows are split into S <= 128 groups
+ * whose fp32 partial products are summed in group order and rounded once, so
+ * results are deterministic.  Workspace: hrm_moe_gate_wgrad_workspace_size.
+ * dtype bf16 or f16.  Limits: E and H multiples of 8, T*H*2 and T*E*2 < 2^32. */
+size_t hrm_moe_gate_wgrad_workspace_size(int64_t num_tokens, int32_t num_experts, int64_t hidden_size);
+int hrm_moe_gate_wgrad(const void* grad_logits, const void* hidden, int64_t num_tokens, int32_t num_experts,
+                       int64_t hidden_size, int dtype, void* grad_gate_weight, void* workspace,
+                       size_t workspace_bytes, void* stream);
+
 /* hrm_moe_grouped_gemm_tn with the B operand's rows gathered:
  *   C[e][Na,Nb] = A[rows_e]^T . B[b_row_index[rows_e]]
  * with B [b_rows, Nb] and b_row_index [M] (values in [0, b_rows); others read

@@ -122,3 +122,19 @@ def test_router_backward_matches_oracle(cuda, t, e, k, norm, with_gp):
     again = ops.router_topk_backward(probs, idx, gw.to(cuda), gp.to(cuda) if gp is not None else None, norm,
                                      torch.bfloat16)
     assert torch.equal(got, again)
+
+
+@pytest.mark.parametrize("t,e,h", [(16384, 64, 1280), (512, 8, 256), (1000, 128, 1536), (100, 16, 264),
+                                   (40000, 64, 1536)])
+def test_gate_wgrad_matches_fp32_product(cuda, t, e, h):
+    """Split-K router gate weight gradient vs one fp32 product rounded once (the F.linear weight grad)."""
+    from oracle import synth
+    dz = torch.from_numpy(synth.normal(t + e, (t, e), std=0.1)).to(torch.bfloat16)
+    x = torch.from_numpy(synth.normal(t + h, (t, h))).to(torch.bfloat16)
+    got = ops.gate_wgrad(dz.to(cuda), x.to(cuda))
+    ref = (dz.float().T @ x.float())
+    d = (got.float().cpu() - ref).abs()
+    rel = d.max().item() / ref.abs().max().item()
+    print(f"gate wgrad T={t} E={e} H={h}: max rel err {rel:.3e}")
+    assert got.shape == (e, h) and rel <= 1e-2
+    assert torch.equal(got, ops.gate_wgrad(dz.to(cuda), x.to(cuda))), "not deterministic"
