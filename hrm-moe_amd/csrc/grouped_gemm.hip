@@ -1606,14 +1606,17 @@ MCfg mgemm_cfg(int64_t M, int E, int64_t w_rows, bool gate_up, bool nn = false) 
     const int n = sscanf(env, "%dx%dx%dx%dx%d", &c.bm, &c.bn, &c.stages, &c.waves, &c.bk);
     if (n >= 3 && mcfg_built(c)) return c;
   }
-  // The gate/up kernel stays on 128 x 128 tiles: its gathered rows measured
-  // slower per cycle on 256 x 256 tiles even with half tiles balancing the
-  // last N tile.
+  // 256 x 256 tiles with 8 waves when experts average >= 256 rows and the
+  // weight rows fill whole tiles (for the gate/up kernel: 2I a multiple of 256;
+  // at XL, I = 512, the layer measured 792 against 814 us, and 1550 against
+  // 1650 us at XL128).  L's gate/up (2I = 896) stays on 128 x 128: with a half
+  // tile for its last N tile it measured no faster.
   // The NN (dgrad) kernel takes 256 x 256 tiles even when its width is not a
   // multiple of 256: at L's dact (N = 448) they measured 203 us against 272 us
   // for 128 x 128 tiles, whose higher LDS and DMA traffic per flop costs more
   // than the idle columns of the last N tile.
-  if (!gate_up && M >= (int64_t)E * 256 && (nn || w_rows % 256 == 0)) return MCfg{256, 256, 2, 8, 64};
+  (void)gate_up;
+  if (M >= (int64_t)E * 256 && (nn || w_rows % 256 == 0)) return MCfg{256, 256, 2, 8, 64};
   return MCfg{128, 128, 2, 4, 64};
 }
 
