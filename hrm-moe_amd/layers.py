@@ -65,10 +65,17 @@ class LinearInit(nn.Module):
         return F.linear(input, self.weight, self.bias)
 
 
-def load_balancing_loss_func(routing_weights: Tensor, selected_experts: Tensor, num_experts: int) -> Tensor:
-    """Qwen-style auxiliary load-balancing loss (models/layers.py:163-170)."""
-    tokens_per_expert = torch.bincount(selected_experts.reshape(-1), minlength=num_experts).to(torch.float32) \
-        / selected_experts.shape[0]
+def load_balancing_loss_func(routing_weights: Tensor, selected_experts: Tensor, num_experts: int,
+                             tokens_per_expert: Optional[Tensor] = None) -> Tensor:
+    """Qwen-style auxiliary load-balancing loss (models/layers.py:163-170).
+
+    ``tokens_per_expert`` may pass in the dispatch kernel's counts, which equal
+    ``bincount(selected_experts, minlength=num_experts)``; bincount on the
+    device would first synchronise with the host to size its output.
+    """
+    if tokens_per_expert is None:
+        tokens_per_expert = torch.bincount(selected_experts.reshape(-1), minlength=num_experts)
+    tokens_per_expert = tokens_per_expert.to(torch.float32) / selected_experts.shape[0]
     router_prob_per_expert = routing_weights.mean(dim=0)
     return torch.sum(tokens_per_expert * router_prob_per_expert) * num_experts
 
@@ -210,12 +217,16 @@ class SparseMoEGroupedExperts(nn.Module):
 
     def compute(self, hidden_states: Tensor, selected_experts: Tensor, routing_weights: Tensor) -> Tensor:
         """Expert output [T,H] for tokens routed by ``selected_experts`` / ``routing_weights`` [T,k]."""
+        return self._compute(hidden_states, selected_experts, routing_weights)[0]
+
+    def _compute(self, hidden_states: Tensor, selected_experts: Tensor, routing_weights: Tensor):
+        """(expert output [T,H], tokens_per_expert [E] int64 from the dispatch, or None when T == 0)."""
         num_tokens = hidden_states.shape[0]
         dtype = hidden_states.dtype
         gate_up_weight = self.gate_up_weight.to(dtype)
         down_weight = self.down_weight.to(dtype)
         if num_tokens == 0:
-            return torch.zeros_like(hidden_states)
+            return torch.zeros_like(hidden_states), None
         routing_weights = routing_weights.to(dtype)
 
         if not self._needs_autograd(hidden_states, routing_weights):
@@ -226,14 +237,15 @@ class SparseMoEGroupedExperts(nn.Module):
             with record_moe_profile_phase("down_gemm"):
                 y = ops.grouped_gemm_nt(act, down_weight, d.tokens_per_expert)
             with record_moe_profile_phase("combine"):
-                return ops.combine(y, d, routing_weights)
+                return ops.combine(y, d, routing_weights), d.tokens_per_expert
 
         if self.fused_backward and hidden_states.shape[1] % 64 == 0:
             # HIP forward and backward of the whole expert block
             with record_moe_profile_phase("dispatch"):
                 d = ops.permute(selected_experts, self.num_experts)
             with record_moe_profile_phase("experts"):
-                return _GroupedExpertsFn.apply(hidden_states, routing_weights, gate_up_weight, down_weight, d)
+                out = _GroupedExpertsFn.apply(hidden_states, routing_weights, gate_up_weight, down_weight, d)
+            return out, d.tokens_per_expert
 
         # hidden sizes that are not a multiple of 64: the reference's composition,
         # with the HIP grouped GEMMs under torch autograd
@@ -253,7 +265,7 @@ class SparseMoEGroupedExperts(nn.Module):
             expert_output = expert_output * sorted_weights[:, None]
             out = torch.zeros_like(hidden_states)
             out.index_add_(0, sorted_token_idx, expert_output.to(dtype))
-        return out
+        return out, d.tokens_per_expert
 
     def forward(self, hidden_states: Tensor, selected_experts: Tensor, routing_weights: Tensor,
                 final_hidden_states: Tensor) -> Tensor:
@@ -325,21 +337,25 @@ class SparseMoESwiGLU(nn.Module):
                 routing_probs, routing_weights, selected_experts = ops.router_topk(
                     router_logits, self.top_k, self.norm_topk_prob, hidden_states.dtype, want_probs=want_aux)
 
-        final_hidden_states = self.experts.compute(hidden_states, selected_experts, routing_weights)
+        final_hidden_states, tokens_per_expert = self.experts._compute(hidden_states, selected_experts,
+                                                                       routing_weights)
 
         if want_aux:
             aux_routing_probs = routing_probs
             aux_selected_experts = selected_experts
+            counts = tokens_per_expert  # the dispatch's counts equal the reference's bincount over all tokens
             if total_seqlen is not None:
                 valid_tokens = int(unwrap_tensor(total_seqlen).item())
                 aux_routing_probs = aux_routing_probs[:valid_tokens]
                 aux_selected_experts = aux_selected_experts[:valid_tokens]
+                counts = None
             with record_moe_profile_phase("aux_metrics"):
-                aux_loss = load_balancing_loss_func(aux_routing_probs, aux_selected_experts, self.num_experts)
+                aux_loss = load_balancing_loss_func(aux_routing_probs, aux_selected_experts, self.num_experts,
+                                                    tokens_per_expert=counts)
                 moe_context.setdefault("aux_losses", []).append(aux_loss)
                 with torch.no_grad():
-                    expert_counts = torch.bincount(aux_selected_experts.reshape(-1),
-                                                   minlength=self.num_experts).to(torch.float32)
-                    moe_context.setdefault("expert_counts", []).append(expert_counts)
+                    if counts is None:
+                        counts = torch.bincount(aux_selected_experts.reshape(-1), minlength=self.num_experts)
+                    moe_context.setdefault("expert_counts", []).append(counts.to(torch.float32))
 
         return final_hidden_states.reshape(original_shape)
