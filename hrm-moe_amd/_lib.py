@@ -50,6 +50,9 @@ PROTOTYPES = {
     "hrm_moe_gate_up_swiglu_save": (_INT, [_P, _P, _P, _P, _I64, _I64, _I64, _I64, _I32, _INT, _P, _P, _P, _SZ, _P]),
     "hrm_moe_down_dgrad_swiglu": (_INT, [_P, _P, _P, _P, _I64, _I64, _I64, _I32, _INT, _P, _P, _SZ, _P]),
     "hrm_moe_combine_backward": (_INT, [_P, _P, _P, _P, _P, _I64, _I32, _I64, _I32, _INT, _P, _P, _P]),
+    "hrm_moe_router_dispatch_workspace_size": (_SZ, [_I64, _I32, _I32]),
+    "hrm_moe_router_topk_dispatch": (_INT, [_P, _INT, _I64, _I32, _I32, _I32, _P, _P, _P, _INT, _P, _P, _P, _P, _P,
+                                            _P, _SZ, _P]),
     "hrm_moe_gate_wgrad_workspace_size": (_SZ, [_I64, _I32, _I64]),
     "hrm_moe_gate_wgrad": (_INT, [_P, _P, _I64, _I32, _I64, _INT, _P, _P, _SZ, _P]),
     "hrm_moe_router_topk_backward": (_INT, [_P, _P, _P, _INT, _P, _I64, _I32, _I32, _I32, _P, _INT, _P]),

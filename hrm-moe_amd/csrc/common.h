@@ -55,6 +55,12 @@ __device__ __forceinline__ void st8(void* p, u32x2 v) { *reinterpret_cast<u32x2*
 
 inline int ceil_div(int64_t a, int64_t b) { return int((a + b - 1) / b); }
 
+// Second dispatch stage (permute.hip), after a rank step that wrote rank[R] and
+// counts[nb][E+1] for rank blocks of SB slots: one scan + scatter launch.
+int dispatch_from_ranks(const int64_t* topk_idx, int64_t R, int E, int k, int SB, int nb, const int32_t* rank,
+                        const int32_t* counts, int64_t* tokens_per_expert, int32_t* expert_offsets,
+                        int32_t* sorted_token_idx, int64_t* sort_idx, int32_t* slot_to_row, void* stream);
+
 }  // namespace hrm
 
 // Launch helper: returns the launch status as an int.

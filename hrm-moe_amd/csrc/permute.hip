@@ -208,7 +208,100 @@ __global__ __launch_bounds__(256) void permute_scatter_kernel(const int64_t* __r
   slot_to_row[s] = row;
 }
 
+// Scan and scatter in one launch, after a rank step that wrote rank[R] and
+// counts[nb][E+1] for rank blocks of SB slots (the router kernel's fused rank
+// step).  Workgroup g handles rank blocks [g*G, g*G+G).  It recomputes, from
+// the whole counts matrix, every bucket's total and its own blocks' prefix:
+// workgroups never wait on one another, and each reads nb*(E+1) ints.
+// Workgroup 0 also writes tokens_per_expert and expert_offsets.  Rows and
+// their order are those of the three-kernel path.  Needs E + 1 <= 512.
+__global__ __launch_bounds__(1024) void permute_scan_scatter_kernel(
+    const int64_t* __restrict__ idx, int64_t R, int E, int k, int SB, int nb, int G, const int32_t* __restrict__ rank,
+    const int32_t* __restrict__ counts, int64_t* __restrict__ tokens_per_expert, int32_t* __restrict__ expert_offsets,
+    int32_t* __restrict__ sorted_token_idx, int64_t* __restrict__ sort_idx, int32_t* __restrict__ slot_to_row) {
+  __shared__ int32_t part[1024];
+  __shared__ int32_t part_pre[1024];
+  __shared__ int32_t tot[513], off[513], base[513];
+  const int nbk = E + 1;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int rb0 = blockIdx.x * G, rb1 = min(nb, rb0 + G);
+  const int NG = 1024 / nbk;  // groups of nbk threads, each summing a range of rows
+  const int per = (nb + NG - 1) / NG;
+  const int b = tid % nbk, g = tid / nbk;
+  const bool on = g < NG;
+  int32_t all = 0, pre = 0;
+  if (on) {
+    const int j0 = g * per, j1 = min(nb, j0 + per);
+    for (int j = j0; j < j1; ++j) {
+      const int32_t c = counts[(int64_t)j * nbk + b];
+      all += c;
+      pre += j < rb0 ? c : 0;
+    }
+  }
+  part[tid] = all;
+  part_pre[tid] = pre;
+  __syncthreads();
+  if (on && g == 0) {
+    int32_t t = 0, p = 0;
+    for (int u = 0; u < NG; ++u) {
+      t += part[u * nbk + b];
+      p += part_pre[u * nbk + b];
+    }
+    tot[b] = t;
+    base[b] = p;
+  }
+  __syncthreads();
+  if (tid < 64) {  // exclusive scan of the bucket totals, 64 at a time
+    int32_t carry = 0;
+    for (int c = 0; c < nbk; c += 64) {
+      const int bb = c + lane;
+      const int32_t v = bb < nbk ? tot[bb] : 0;
+      const int32_t incl = wave_incl_scan(v, lane);
+      if (bb < nbk) off[bb] = carry + incl - v;
+      carry += __shfl(incl, 63, 64);
+    }
+  }
+  __syncthreads();
+  if (tid < nbk) {
+    base[tid] += off[tid];
+    if (blockIdx.x == 0) {
+      if (tid < E) tokens_per_expert[tid] = (int64_t)tot[tid];
+      expert_offsets[tid] = off[tid];  // expert_offsets[E] = start of the dropped rows
+    }
+  }
+  __syncthreads();
+  for (int rb = rb0; rb < rb1; ++rb) {
+    for (int ls = tid; ls < SB; ls += 1024) {
+      const int64_t sl = (int64_t)rb * SB + ls;
+      if (sl < R) {
+        const int bk = bucket_of(idx[sl], E);
+        const int32_t row = base[bk] + rank[sl];
+        sorted_token_idx[row] = (int32_t)(sl / k);
+        if (sort_idx) sort_idx[row] = sl;
+        slot_to_row[sl] = row;
+      }
+    }
+    __syncthreads();
+    if (tid < nbk) base[tid] += counts[(int64_t)rb * nbk + tid];
+    __syncthreads();
+  }
+}
+
 }  // namespace
+
+// Second dispatch stage after a rank step that wrote rank[R] and counts[nb][E+1]
+// with SB slots per rank block (used by the router's fused entry point).
+int dispatch_from_ranks(const int64_t* topk_idx, int64_t R, int E, int k, int SB, int nb, const int32_t* rank,
+                        const int32_t* counts, int64_t* tokens_per_expert, int32_t* expert_offsets,
+                        int32_t* sorted_token_idx, int64_t* sort_idx, int32_t* slot_to_row, void* stream) {
+  if (E + 1 > 512) return HRM_MOE_ERR_UNSUPPORTED;
+  const int G = nb <= 32 ? 1 : (nb + 31) / 32;
+  const int blocks = nb == 0 ? 1 : (nb + G - 1) / G;
+  HRM_LAUNCH(permute_scan_scatter_kernel, dim3(blocks), dim3(1024), 0, stream, topk_idx, R, E, k, SB, nb, G, rank,
+             counts, tokens_per_expert, expert_offsets, sorted_token_idx, sort_idx, slot_to_row);
+  return HRM_MOE_OK;
+}
+
 }  // namespace hrm
 
 extern "C" size_t hrm_moe_permute_workspace_size(int64_t num_tokens, int32_t num_experts, int32_t top_k) {

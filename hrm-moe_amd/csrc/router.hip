@@ -30,6 +30,8 @@
 namespace hrm {
 namespace {
 
+constexpr int kRouterMaxExperts = 128;
+
 // Value of the lane at distance D inside the row (D = 1, 2: xor; D = 4, 8:
 // rotation within a row of 16 lanes).
 template <int D>
@@ -84,11 +86,19 @@ __device__ __forceinline__ void select_round(uint32_t (&key)[C], int e0, uint32_
 }
 
 // KFIX: k == SLOTS, known at compile time (the usual top-2/4/8).
-template <int NP2, int SLOTS, int LPR, bool KFIX>
+// RANK (k <= 8 only): also the first step of the dispatch for this block's
+// RPB * k routed slots (flat index row * k + j): each slot's rank among the
+// block's slots of the same expert bucket (bucket E holds ids outside [0, E)),
+// and the block's per-bucket counts, counts[blockIdx.x][E + 1].  Same method
+// as the dispatch's rank kernel (LDS bitmask per bucket, rank = popcount of
+// the lower bits), so the stable order does not depend on atomic ordering.
+template <int NP2, int SLOTS, int LPR, bool KFIX, bool RANK = false>
 __global__ __launch_bounds__(256) void router_topk_kernel(const void* __restrict__ logits, int ldt, int64_t T, int E,
                                                           int k_rt, int norm, float* __restrict__ probs,
                                                           int64_t* __restrict__ idx_out, void* __restrict__ w_out,
-                                                          int wdt) {
+                                                          int wdt, int32_t* __restrict__ rank_out,
+                                                          int32_t* __restrict__ counts_out) {
+  static_assert(!RANK || SLOTS <= 8, "the fused rank step runs in the register (k <= 8) path");
   constexpr int C = NP2 / LPR;
   constexpr int RPB = 256 / LPR;  // rows per block
   constexpr int KC = KFIX ? SLOTS : 0;
@@ -184,7 +194,7 @@ __global__ __launch_bounds__(256) void router_topk_kernel(const void* __restrict
       si[r] = 0;
       if (r < k) select_round<C, LPR>(key, e0, sk[r], si[r]);
     }
-    if (!active) return;
+    if (!RANK && !active) return;  // with RANK every thread reaches the block barriers below
     uint32_t gk[SLOTS];
     int gi[SLOTS];
     torch_topk_order<SLOTS, KC>(sk, si, k, gk, gi);
@@ -199,9 +209,45 @@ __global__ __launch_bounds__(256) void router_topk_kernel(const void* __restrict
     }
 #pragma unroll
     for (int j = 0; j < SLOTS; ++j) {
-      if (j < k && (j % LPR) == q) {
+      if (active && j < k && (j % LPR) == q) {
         idx_out[row * k + j] = (int64_t)gi[j];
         store_weight(w_out, wdt, row * k + j, w[j]);
+      }
+    }
+    if constexpr (RANK) {
+      constexpr int SBMAX = RPB * 8;
+      __shared__ uint32_t s_mask[(kRouterMaxExperts + 1) * (SBMAX / 32)];
+      __shared__ uint32_t s_pref[(kRouterMaxExperts + 1) * (SBMAX / 32)];
+      const int nbk = E + 1;
+      const int words = (RPB * k + 31) / 32;
+      for (int i = threadIdx.x; i < nbk * words; i += 256) s_mask[i] = 0u;
+      __syncthreads();
+#pragma unroll
+      for (int j = 0; j < SLOTS; ++j) {
+        if (active && j < k && (j % LPR) == q) {
+          const int ls = lr * k + j;
+          const int b = (gi[j] >= 0 && gi[j] < E) ? gi[j] : E;
+          atomicOr(&s_mask[b * words + (ls >> 5)], 1u << (ls & 31));
+        }
+      }
+      __syncthreads();
+      for (int b = threadIdx.x; b < nbk; b += 256) {
+        uint32_t run = 0;
+        for (int w2 = 0; w2 < words; ++w2) {
+          s_pref[b * words + w2] = run;
+          run += __popc(s_mask[b * words + w2]);
+        }
+        counts_out[(int64_t)blockIdx.x * nbk + b] = (int32_t)run;
+      }
+      __syncthreads();
+#pragma unroll
+      for (int j = 0; j < SLOTS; ++j) {
+        if (active && j < k && (j % LPR) == q) {
+          const int ls = lr * k + j;
+          const int b = (gi[j] >= 0 && gi[j] < E) ? gi[j] : E;
+          const uint32_t below = s_mask[b * words + (ls >> 5)] & ((1u << (ls & 31)) - 1u);
+          rank_out[row * k + j] = (int32_t)(s_pref[b * words + (ls >> 5)] + __popc(below));
+        }
       }
     }
   } else {
@@ -236,13 +282,34 @@ __global__ __launch_bounds__(256) void router_topk_kernel(const void* __restrict
   }
 }
 
+// Router with the fused rank step (k <= 8): RPB * k slots per rank block.
+template <int NP2>
+int launch_router_rank(const void* logits, int ldt, int64_t T, int E, int k, int norm, float* probs, int64_t* idx,
+                       void* w, int wdt, int32_t* rank, int32_t* counts, void* stream) {
+  constexpr int LPR = 4, RPB = 256 / LPR;
+  dim3 grid((unsigned)((T + RPB - 1) / RPB)), block(256);
+#define HRM_RTR(SL, KF)                                                                                              \
+  HRM_LAUNCH((router_topk_kernel<NP2, SL, LPR, KF, true>), grid, block, 0, stream, logits, ldt, T, E, k, norm, probs, \
+             idx, w, wdt, rank, counts)
+  if (k == 2) HRM_RTR(2, true);
+  else if (k == 4) HRM_RTR(4, true);
+  else if (k == 8) HRM_RTR(8, true);
+  else if (k <= 2) HRM_RTR(2, false);
+  else if (k <= 4) HRM_RTR(4, false);
+  else if (k <= 8) HRM_RTR(8, false);
+  else return HRM_MOE_ERR_UNSUPPORTED;
+#undef HRM_RTR
+  return HRM_MOE_OK;
+}
+
 template <int NP2, int LPR>
 int launch_router_np2(const void* logits, int ldt, int64_t T, int E, int k, int norm, float* probs, int64_t* idx,
                       void* w, int wdt, void* stream) {
   constexpr int RPB = 256 / LPR;
   dim3 grid((unsigned)((T + RPB - 1) / RPB)), block(256);
-#define HRM_RT(SL, KF) \
-  HRM_LAUNCH((router_topk_kernel<NP2, SL, LPR, KF>), grid, block, 0, stream, logits, ldt, T, E, k, norm, probs, idx, w, wdt)
+#define HRM_RT(SL, KF)                                                                                              \
+  HRM_LAUNCH((router_topk_kernel<NP2, SL, LPR, KF>), grid, block, 0, stream, logits, ldt, T, E, k, norm, probs, idx, w, \
+             wdt, (int32_t*)nullptr, (int32_t*)nullptr)
   if (k == 2) HRM_RT(2, true);
   else if (k == 4) HRM_RT(4, true);
   else if (k == 8) HRM_RT(8, true);
@@ -352,4 +419,62 @@ extern "C" int hrm_moe_router_topk_backward(const float* probs, const int64_t* t
                      norm_topk_prob, grad_logits, logits_dtype);
   const hipError_t err = hipGetLastError();
   return err == hipSuccess ? HRM_MOE_OK : (int)err;
+}
+
+// Router + dispatch in two launches: the router kernel with its fused rank step,
+// then one scan + scatter kernel.  Outputs are those of hrm_moe_router_topk
+// followed by hrm_moe_permute on its topk_idx.
+namespace hrm {
+namespace {
+inline int64_t router_dispatch_blocks(int64_t T) { return (T + 63) / 64; }  // 64 rows per router block
+inline size_t router_dispatch_ws(int64_t T, int E, int k) {
+  const size_t r = (size_t)T * (size_t)k;
+  return ((sizeof(int32_t) * r + 255) & ~size_t(255)) +
+         ((sizeof(int32_t) * (size_t)router_dispatch_blocks(T) * (size_t)(E + 1) + 255) & ~size_t(255)) + 256;
+}
+}  // namespace
+}  // namespace hrm
+
+extern "C" size_t hrm_moe_router_dispatch_workspace_size(int64_t num_tokens, int32_t num_experts, int32_t top_k) {
+  if (num_tokens < 0 || num_experts < 1 || num_experts > 128 || top_k < 1 || top_k > 8) return 0;
+  return hrm::router_dispatch_ws(num_tokens, num_experts, top_k);
+}
+
+extern "C" int hrm_moe_router_topk_dispatch(const void* logits, int logits_dtype, int64_t num_tokens,
+                                            int32_t num_experts, int32_t top_k, int32_t norm_topk_prob, float* probs,
+                                            int64_t* topk_idx, void* topk_weight, int weight_dtype,
+                                            int64_t* tokens_per_expert, int32_t* expert_offsets,
+                                            int32_t* sorted_token_idx, int64_t* sort_idx, int32_t* slot_to_row,
+                                            void* workspace, size_t workspace_bytes, void* stream) {
+  if (num_tokens < 0 || num_experts < 1 || top_k < 1 || top_k > num_experts) return HRM_MOE_ERR_INVALID;
+  if (logits_dtype < HRM_MOE_BF16 || logits_dtype > HRM_MOE_F32) return HRM_MOE_ERR_DTYPE;
+  if (weight_dtype < HRM_MOE_BF16 || weight_dtype > HRM_MOE_F32) return HRM_MOE_ERR_DTYPE;
+  if (num_experts > 128 || top_k > 8 || num_tokens * top_k >= (int64_t(1) << 31)) return HRM_MOE_ERR_UNSUPPORTED;
+  if (!tokens_per_expert || !expert_offsets) return HRM_MOE_ERR_INVALID;
+  if (num_tokens > 0 && (!logits || !topk_idx || !topk_weight || !sorted_token_idx || !slot_to_row))
+    return HRM_MOE_ERR_INVALID;
+  if (!workspace || workspace_bytes < hrm::router_dispatch_ws(num_tokens, num_experts, top_k))
+    return HRM_MOE_ERR_WORKSPACE;
+  const int E = num_experts, k = top_k;
+  const int64_t R = num_tokens * k;
+  const int nb = (int)hrm::router_dispatch_blocks(num_tokens);
+  char* p = static_cast<char*>(workspace);
+  int32_t* rank = reinterpret_cast<int32_t*>(p);
+  p += (sizeof(int32_t) * (size_t)R + 255) & ~size_t(255);
+  int32_t* counts = reinterpret_cast<int32_t*>(p);
+  if (num_tokens > 0) {
+    int st;
+    if (E <= 8)
+      st = hrm::launch_router_rank<8>(logits, logits_dtype, num_tokens, E, k, norm_topk_prob, probs, topk_idx,
+                                      topk_weight, weight_dtype, rank, counts, stream);
+    else if (E <= 64)
+      st = hrm::launch_router_rank<64>(logits, logits_dtype, num_tokens, E, k, norm_topk_prob, probs, topk_idx,
+                                       topk_weight, weight_dtype, rank, counts, stream);
+    else
+      st = hrm::launch_router_rank<128>(logits, logits_dtype, num_tokens, E, k, norm_topk_prob, probs, topk_idx,
+                                        topk_weight, weight_dtype, rank, counts, stream);
+    if (st) return st;
+  }
+  return hrm::dispatch_from_ranks(topk_idx, R, E, k, 64 * k, nb, rank, counts, tokens_per_expert, expert_offsets,
+                                  sorted_token_idx, sort_idx, slot_to_row, stream);
 }

@@ -219,8 +219,13 @@ class SparseMoEGroupedExperts(nn.Module):
         """Expert output [T,H] for tokens routed by ``selected_experts`` / ``routing_weights`` [T,k]."""
         return self._compute(hidden_states, selected_experts, routing_weights)[0]
 
-    def _compute(self, hidden_states: Tensor, selected_experts: Tensor, routing_weights: Tensor):
-        """(expert output [T,H], tokens_per_expert [E] int64 from the dispatch, or None when T == 0)."""
+    def _compute(self, hidden_states: Tensor, selected_experts: Tensor, routing_weights: Tensor,
+                 dispatch: Optional["ops.Dispatch"] = None):
+        """(expert output [T,H], tokens_per_expert [E] int64 from the dispatch, or None when T == 0).
+
+        ``dispatch``: the permutation of ``selected_experts`` when the caller
+        already has it (the router's fused dispatch); used on the no-autograd path.
+        """
         num_tokens = hidden_states.shape[0]
         dtype = hidden_states.dtype
         gate_up_weight = self.gate_up_weight.to(dtype)
@@ -231,7 +236,7 @@ class SparseMoEGroupedExperts(nn.Module):
 
         if not self._needs_autograd(hidden_states, routing_weights):
             with record_moe_profile_phase("dispatch"):
-                d = ops.permute(selected_experts, self.num_experts)
+                d = dispatch if dispatch is not None else ops.permute(selected_experts, self.num_experts)
             with record_moe_profile_phase("gate_up_gemm"):
                 act = ops.gate_up_swiglu(hidden_states, d, gate_up_weight)
             with record_moe_profile_phase("down_gemm"):
@@ -321,6 +326,7 @@ class SparseMoESwiGLU(nn.Module):
         hidden_states = x.reshape(-1, self.hidden_size)
         want_aux = moe_context is not None and torch.is_grad_enabled()
 
+        dispatch = None
         with record_moe_profile_phase("router"):
             w_gate = self.gate.weight
             if (torch.is_grad_enabled() and w_gate.requires_grad and self.gate.bias is None
@@ -333,12 +339,17 @@ class SparseMoESwiGLU(nn.Module):
             if torch.is_grad_enabled() and router_logits.requires_grad:
                 routing_probs, routing_weights, selected_experts = _RouterTopK.apply(
                     router_logits, self.top_k, self.norm_topk_prob, hidden_states.dtype)
+            elif self.num_experts <= 128 and self.top_k <= 8 and not self.experts._needs_autograd(
+                    hidden_states, router_logits):
+                # router and dispatch in two launches
+                routing_probs, routing_weights, selected_experts, dispatch = ops.router_topk_dispatch(
+                    router_logits, self.top_k, self.norm_topk_prob, hidden_states.dtype, want_probs=want_aux)
             else:
                 routing_probs, routing_weights, selected_experts = ops.router_topk(
                     router_logits, self.top_k, self.norm_topk_prob, hidden_states.dtype, want_probs=want_aux)
 
         final_hidden_states, tokens_per_expert = self.experts._compute(hidden_states, selected_experts,
-                                                                       routing_weights)
+                                                                       routing_weights, dispatch)
 
         if want_aux:
             aux_routing_probs = routing_probs

@@ -224,6 +224,38 @@ def grouped_gemm_tn(a: torch.Tensor, b: torch.Tensor, tokens_per_expert: torch.T
     return c
 
 
+def router_topk_dispatch(logits: torch.Tensor, top_k: int, norm_topk_prob: bool, weight_dtype: torch.dtype,
+                         want_probs: bool = True, want_sort_idx: bool = False):
+    """router_topk then permute, in two launches: (probs or None, weights [T,k], idx [T,k], Dispatch).
+
+    Needs E <= 128 and k <= 8 (the fused rank step); callers fall back to the two ops otherwise.
+    """
+    dev = _require_cuda(logits)
+    if logits.dim() != 2:
+        raise ValueError(f"router logits must be [tokens, experts], got {tuple(logits.shape)}")
+    logits = logits.contiguous()
+    t, e = logits.shape
+    r = t * top_k
+    probs = torch.empty((t, e), dtype=torch.float32, device=dev) if want_probs else None
+    idx = torch.empty((t, top_k), dtype=torch.int64, device=dev)
+    w = torch.empty((t, top_k), dtype=weight_dtype, device=dev)
+    tpe = torch.empty(e, dtype=torch.int64, device=dev)
+    offsets = torch.empty(e + 1, dtype=torch.int32, device=dev)
+    sorted_token_idx = torch.empty(r, dtype=torch.int32, device=dev)
+    slot_to_row = torch.empty(r, dtype=torch.int32, device=dev)
+    sort_idx = torch.empty(r, dtype=torch.int64, device=dev) if want_sort_idx else None
+    lib = _lib.lib()
+    ws = _workspace(lib.hrm_moe_router_dispatch_workspace_size(t, e, top_k), dev)
+    with _lib.device_guard(dev):
+        st = lib.hrm_moe_router_topk_dispatch(
+            _lib.ptr(logits), _lib.dtype_code(logits.dtype), t, e, top_k, int(bool(norm_topk_prob)), _lib.ptr(probs),
+            _lib.ptr(idx), _lib.ptr(w), _lib.dtype_code(weight_dtype), _lib.ptr(tpe), _lib.ptr(offsets),
+            _lib.ptr(sorted_token_idx), _lib.ptr(sort_idx), _lib.ptr(slot_to_row), _lib.ptr(ws), ws.numel(),
+            _lib.stream_of(dev))
+    _lib.check(st, "router_topk_dispatch")
+    return probs, w, idx, Dispatch(tpe, offsets, sorted_token_idx, slot_to_row, sort_idx)
+
+
 def grouped_gemm_tn_gather(a: torch.Tensor, b: torch.Tensor, b_row_index: torch.Tensor,
                            tokens_per_expert: torch.Tensor) -> torch.Tensor:
     """C[e][Na,Nb] = A[rows_e]^T @ B[b_row_index[rows_e]]: wgrad over gathered B rows (B [b_rows, Nb])."""

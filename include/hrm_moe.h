@@ -85,6 +85,22 @@ int hrm_moe_permute(const int64_t* topk_idx, int64_t num_tokens, int32_t num_exp
                     void* stream);
 
 /*
+ * Router and dispatch in two launches: hrm_moe_router_topk, then
+ * hrm_moe_permute on its topk_idx, with the same outputs.  The router kernel
+ * also ranks each block's routed slots within their expert, and one
+ * scan + scatter kernel finishes the dispatch.  Replaces models/layers.py:
+ * 606-610 and :312-322 back to back.  sort_idx may be NULL.
+ * Limits: E <= 128, k <= 8, T*k < 2^31.  Workspace:
+ * hrm_moe_router_dispatch_workspace_size.
+ */
+size_t hrm_moe_router_dispatch_workspace_size(int64_t num_tokens, int32_t num_experts, int32_t top_k);
+int hrm_moe_router_topk_dispatch(const void* logits, int logits_dtype, int64_t num_tokens, int32_t num_experts,
+                                 int32_t top_k, int32_t norm_topk_prob, float* probs, int64_t* topk_idx,
+                                 void* topk_weight, int weight_dtype, int64_t* tokens_per_expert,
+                                 int32_t* expert_offsets, int32_t* sorted_token_idx, int64_t* sort_idx,
+                                 int32_t* slot_to_row, void* workspace, size_t workspace_bytes, void* stream);
+
+/*
  * Grouped GEMMs over expert-contiguous row groups: rows
  * [sum(tpe[:e]), sum(tpe[:e+1])) belong to expert e.  tokens_per_expert is
  * int64 on the device and is never read on the host.  fp32 accumulation,

@@ -112,6 +112,17 @@ def test_training_entry_points_reject_bad_arguments():
     assert gw(buf, buf, 16384, 60, 1280, _lib.BF16, buf, buf, gws, NULL) == _lib.ERR_UNSUPPORTED
     assert gw(buf, buf, 16384, 64, 1280, _lib.F32, buf, buf, gws, NULL) == _lib.ERR_DTYPE
     assert gw(NULL, buf, 16384, 64, 1280, _lib.BF16, buf, buf, gws, NULL) == _lib.ERR_INVALID
+    assert lib.hrm_moe_router_dispatch_workspace_size(16, 200, 8) == 0
+    rd = lib.hrm_moe_router_topk_dispatch
+    rws = lib.hrm_moe_router_dispatch_workspace_size(16, 64, 8)
+    assert rd(buf, _lib.BF16, 16, 64, 16, 1, buf, buf, buf, _lib.BF16, buf, buf, buf, NULL, buf, buf, rws,
+              NULL) == _lib.ERR_UNSUPPORTED
+    assert rd(buf, _lib.BF16, 16, 64, 8, 1, buf, buf, buf, _lib.BF16, buf, buf, buf, NULL, buf, buf, rws - 1,
+              NULL) == _lib.ERR_WORKSPACE
+    assert rd(buf, _lib.BF16, 16, 64, 8, 1, buf, NULL, buf, _lib.BF16, buf, buf, buf, NULL, buf, buf, rws,
+              NULL) == _lib.ERR_INVALID
+    assert rd(buf, 7, 16, 64, 8, 1, buf, buf, buf, _lib.BF16, buf, buf, buf, NULL, buf, buf, rws,
+              NULL) == _lib.ERR_DTYPE
     rb = lib.hrm_moe_router_topk_backward
     assert rb(buf, buf, buf, _lib.BF16, NULL, 16, 200, 8, 1, buf, _lib.BF16, NULL) == _lib.ERR_UNSUPPORTED
     assert rb(buf, buf, buf, 9, NULL, 16, 64, 8, 1, buf, _lib.BF16, NULL) == _lib.ERR_DTYPE

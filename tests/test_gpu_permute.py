@@ -72,3 +72,30 @@ def test_permute_out_of_range_ids_go_last(cuda):
     valid = int((bucket < 16).sum())
     assert d.expert_offsets.cpu().numpy()[-1] == valid
     assert d.tokens_per_expert.sum().item() == valid
+
+
+@pytest.mark.parametrize("t,e,k,skew", [(1, 64, 8, 0.0), (8, 64, 8, 0.0), (100, 8, 2, 0.0), (4096, 64, 8, 1.5),
+                                         (16384, 64, 8, 0.0), (333, 128, 8, 0.0), (1000, 16, 1, 0.0),
+                                         (777, 32, 3, 2.0), (2048, 64, 4, 0.0)])
+def test_router_dispatch_matches_router_then_permute(cuda, t, e, k, skew):
+    """The two-launch router + dispatch gives the bits of router_topk followed by permute."""
+    from oracle import synth
+    rng = np.random.default_rng(t + e + k)
+    logits = torch.from_numpy(rng.standard_normal((t, e)).astype(np.float32) +
+                              (rng.standard_normal(e).astype(np.float32) * skew)[None, :]).to(torch.bfloat16)
+    lg = logits.to(cuda)
+    probs, w, idx, d = ops.router_topk_dispatch(lg, k, True, torch.bfloat16, want_probs=True, want_sort_idx=True)
+    probs2, w2, idx2 = ops.router_topk(lg, k, True, torch.bfloat16)
+    d2 = ops.permute(idx2, e, want_sort_idx=True)
+    assert torch.equal(idx, idx2) and torch.equal(w, w2) and torch.equal(probs, probs2)
+    for name in ("tokens_per_expert", "expert_offsets", "sorted_token_idx", "slot_to_row", "sort_idx"):
+        assert torch.equal(getattr(d, name), getattr(d2, name)), name
+    ref = mo.permute(idx.cpu().numpy(), e)
+    assert np.array_equal(d.sort_idx.cpu().numpy(), ref["sort_idx"])
+
+
+def test_router_dispatch_zero_tokens(cuda):
+    lg = torch.zeros((0, 64), dtype=torch.bfloat16, device=cuda)
+    _, w, idx, d = ops.router_topk_dispatch(lg, 8, True, torch.bfloat16, want_probs=False)
+    assert idx.shape == (0, 8) and int(d.tokens_per_expert.abs().sum()) == 0
+    assert int(d.expert_offsets.abs().sum()) == 0
