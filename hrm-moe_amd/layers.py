@@ -116,15 +116,25 @@ class _RouterTopK(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, logits: Tensor, top_k: int, norm_topk_prob: bool, out_dtype: torch.dtype):
-        probs, w, idx = ops.router_topk(logits, top_k, norm_topk_prob, out_dtype, want_probs=True)
+        """(probs, weights, idx, tokens_per_expert, expert_offsets, sorted_token_idx, slot_to_row).
+
+        The dispatch tensors come from the router's fused dispatch when E <= 128
+        and k <= 8, else from the permute kernel.
+        """
+        if logits.shape[1] <= 128 and top_k <= 8:
+            probs, w, idx, d = ops.router_topk_dispatch(logits, top_k, norm_topk_prob, out_dtype, want_probs=True)
+        else:
+            probs, w, idx = ops.router_topk(logits, top_k, norm_topk_prob, out_dtype, want_probs=True)
+            d = ops.permute(idx, logits.shape[1])
         ctx.save_for_backward(probs, idx)
         ctx.norm = norm_topk_prob
         ctx.logits_dtype = logits.dtype
-        ctx.mark_non_differentiable(idx)
-        return probs, w, idx
+        extra = (d.tokens_per_expert, d.expert_offsets, d.sorted_token_idx, d.slot_to_row)
+        ctx.mark_non_differentiable(idx, *extra)
+        return (probs, w, idx) + extra
 
     @staticmethod
-    def backward(ctx, g_probs, g_w, _g_idx):
+    def backward(ctx, g_probs, g_w, _g_idx, *_g_dispatch):
         probs, idx = ctx.saved_tensors
         if g_w is None:
             g_w = torch.zeros(idx.shape, dtype=torch.float32, device=probs.device)
@@ -224,7 +234,8 @@ class SparseMoEGroupedExperts(nn.Module):
         """(expert output [T,H], tokens_per_expert [E] int64 from the dispatch, or None when T == 0).
 
         ``dispatch``: the permutation of ``selected_experts`` when the caller
-        already has it (the router's fused dispatch); used on the no-autograd path.
+        already has it (the router's fused dispatch); the reference-composition
+        path (which needs ``sort_idx``) computes its own.
         """
         num_tokens = hidden_states.shape[0]
         dtype = hidden_states.dtype
@@ -247,7 +258,7 @@ class SparseMoEGroupedExperts(nn.Module):
         if self.fused_backward and hidden_states.shape[1] % 64 == 0:
             # HIP forward and backward of the whole expert block
             with record_moe_profile_phase("dispatch"):
-                d = ops.permute(selected_experts, self.num_experts)
+                d = dispatch if dispatch is not None else ops.permute(selected_experts, self.num_experts)
             with record_moe_profile_phase("experts"):
                 out = _GroupedExpertsFn.apply(hidden_states, routing_weights, gate_up_weight, down_weight, d)
             return out, d.tokens_per_expert
@@ -337,8 +348,9 @@ class SparseMoESwiGLU(nn.Module):
             else:
                 router_logits = self.gate(hidden_states)
             if torch.is_grad_enabled() and router_logits.requires_grad:
-                routing_probs, routing_weights, selected_experts = _RouterTopK.apply(
+                routing_probs, routing_weights, selected_experts, *dd = _RouterTopK.apply(
                     router_logits, self.top_k, self.norm_topk_prob, hidden_states.dtype)
+                dispatch = ops.Dispatch(*dd, None)
             elif self.num_experts <= 128 and self.top_k <= 8 and not self.experts._needs_autograd(
                     hidden_states, router_logits):
                 # router and dispatch in two launches
