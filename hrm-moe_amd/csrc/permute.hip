@@ -215,6 +215,7 @@ __global__ __launch_bounds__(256) void permute_scatter_kernel(const int64_t* __r
 // workgroups never wait on one another, and each reads nb*(E+1) ints.
 // Workgroup 0 also writes tokens_per_expert and expert_offsets.  Rows and
 // their order are those of the three-kernel path.  Needs E + 1 <= 512.
+constexpr int kScatterChunk = 16;  // rank blocks scattered together
 __global__ __launch_bounds__(1024) void permute_scan_scatter_kernel(
     const int64_t* __restrict__ idx, int64_t R, int E, int k, int SB, int nb, int G, const int32_t* __restrict__ rank,
     const int32_t* __restrict__ counts, int64_t* __restrict__ tokens_per_expert, int32_t* __restrict__ expert_offsets,
@@ -222,6 +223,7 @@ __global__ __launch_bounds__(1024) void permute_scan_scatter_kernel(
   __shared__ int32_t part[1024];
   __shared__ int32_t part_pre[1024];
   __shared__ int32_t tot[513], off[513], base[513];
+  __shared__ int32_t cbase[kScatterChunk][513];
   const int nbk = E + 1;
   const int tid = threadIdx.x, lane = tid & 63;
   const int rb0 = blockIdx.x * G, rb1 = min(nb, rb0 + G);
@@ -232,6 +234,7 @@ __global__ __launch_bounds__(1024) void permute_scan_scatter_kernel(
   int32_t all = 0, pre = 0;
   if (on) {
     const int j0 = g * per, j1 = min(nb, j0 + per);
+#pragma unroll 8
     for (int j = j0; j < j1; ++j) {
       const int32_t c = counts[(int64_t)j * nbk + b];
       all += c;
@@ -270,19 +273,35 @@ __global__ __launch_bounds__(1024) void permute_scan_scatter_kernel(
     }
   }
   __syncthreads();
-  for (int rb = rb0; rb < rb1; ++rb) {
-    for (int ls = tid; ls < SB; ls += 1024) {
-      const int64_t sl = (int64_t)rb * SB + ls;
+  // Scatter, kScatterChunk rank blocks at a time: first each bucket's start
+  // row in every rank block of the chunk (a running sum over the chunk's
+  // counts), then every slot of the chunk at once.
+  for (int c0 = rb0; c0 < rb1; c0 += kScatterChunk) {
+    const int n = min(kScatterChunk, rb1 - c0);
+    if (tid < nbk) {
+      int32_t cnt[kScatterChunk];
+#pragma unroll
+      for (int i = 0; i < kScatterChunk; ++i) cnt[i] = i < n ? counts[(int64_t)(c0 + i) * nbk + tid] : 0;
+      int32_t run = base[tid];
+#pragma unroll
+      for (int i = 0; i < kScatterChunk; ++i) {
+        cbase[i][tid] = run;
+        run += cnt[i];
+      }
+      base[tid] = run;
+    }
+    __syncthreads();
+    for (int it = tid; it < n * SB; it += 1024) {
+      const int i = it / SB;
+      const int64_t sl = (int64_t)c0 * SB + it;
       if (sl < R) {
         const int bk = bucket_of(idx[sl], E);
-        const int32_t row = base[bk] + rank[sl];
+        const int32_t row = cbase[i][bk] + rank[sl];
         sorted_token_idx[row] = (int32_t)(sl / k);
         if (sort_idx) sort_idx[row] = sl;
         slot_to_row[sl] = row;
       }
     }
-    __syncthreads();
-    if (tid < nbk) base[tid] += counts[(int64_t)rb * nbk + tid];
     __syncthreads();
   }
 }
