@@ -85,7 +85,7 @@ class OpTimer:
     op's kernels.
     """
 
-    NAMES = ("router_topk", "permute", "gate_up_swiglu", "grouped_gemm_nt", "combine")
+    NAMES = ("router_topk", "permute", "router_topk_dispatch", "gate_up_swiglu", "grouped_gemm_nt", "combine")
 
     def __init__(self, ops):
         self.ops = ops
@@ -424,8 +424,8 @@ def main():
 
     op_ms = timer.mean_ms()
     phases = {
-        "router": op_ms["router_topk"],
-        "dispatch": op_ms["permute"],
+        # one fused call (router + dispatch) for E <= 128 and k <= 8, else two
+        "router_and_dispatch": op_ms["router_topk"] + op_ms["permute"] + op_ms["router_topk_dispatch"],
         "gate_up_swiglu": op_ms["gate_up_swiglu"],
         "down_gemm": op_ms["grouped_gemm_nt"],
         "combine": op_ms["combine"],
