@@ -622,7 +622,8 @@ __device__ __forceinline__ u32x4 bload16(__amdgpu_buffer_rsrc_t r, uint32_t voff
 // Non-temporal (nt) policy for stores of output that nothing re-reads from L2
 // soon.  The persistent kernels' first wait of the next tile also waits for
 // the previous tile's stores, and nt stores are acknowledged sooner: the NT
-// GEMM at L (131072 x 1280 x 448) measured 177 against 204 us.
+// GEMM at L (131072 x 1280 x 448) measured 177 against 204 us, and the L
+// training step (dgrad and wgrad outputs too) 2384 against 2398 us.
 constexpr int kStoreNT = 2;
 __device__ __forceinline__ void bstore8(__amdgpu_buffer_rsrc_t r, uint32_t voff, u32x2 v) {
   __builtin_amdgcn_raw_buffer_store_b64(v, r, voff, 0, 0);
@@ -1038,8 +1039,10 @@ __global__ __launch_bounds__(NW * 64, NW == 4 ? 2 : 1) void mgemm_dma_kernel(con
             bstore16(rC, xoff + (uint32_t)N * 2, duv);
           } else if (pass == 0) {
             const uint32_t voff = c < N ? (ml * (uint32_t)N + (uint32_t)c) * 2 : 0x80000000u;
-            // the down projection's rows go to the combine, which reads them from HBM
-            bstore16<KIND == KIND_NT ? kStoreNT : 0>(rC, voff, v);
+            // the down projection's rows (and dgrad's d(hidden) rows) go to the combine /
+            // un-permute, which reads them from HBM; the gate/up kernel's act rows
+            // are re-read by the down GEMM right away
+            bstore16<(KIND == KIND_NT || KIND == KIND_NN) ? kStoreNT : 0>(rC, voff, v);
           } else {
             // EPI_SAVE_GU: gate to columns [0, N), up to [N, 2N) of aux
             const uint32_t xoff =
@@ -1387,7 +1390,7 @@ __global__ __launch_bounds__(NW * 64, 1) void wgrad_dma8_kernel(const uint16_t* 
           const uint32_t ml = (uint32_t)(wm * (BA / 2) + p0 * 32 + r);
           const int c = col0 + c16 * 8;
           const uint32_t voff = c < Nb ? (ml * (uint32_t)Nb + (uint32_t)c) * 2 : 0x80000000u;
-          bstore16(rC, voff, v);
+          bstore16<kStoreNT>(rC, voff, v);  // weight gradients: written once, read by the optimizer
         }
       }
     }
