@@ -92,12 +92,25 @@ __device__ __forceinline__ void select_round(uint32_t (&key)[C], int e0, uint32_
 // and the block's per-bucket counts, counts[blockIdx.x][E + 1].  Same method
 // as the dispatch's rank kernel (LDS bitmask per bucket, rank = popcount of
 // the lower bits), so the stable order does not depend on atomic ordering.
-template <int NP2, int SLOTS, int LPR, bool KFIX, bool RANK = false>
+// Outputs of the whole dispatch, written by a single-block launch (SOLO).
+struct DispatchOut {
+  int64_t* tokens_per_expert;
+  int32_t* expert_offsets;
+  int32_t* sorted_token_idx;
+  int64_t* sort_idx;
+  int32_t* slot_to_row;
+};
+
+// SOLO (with RANK, one block, T <= 64): the block's counts are the totals, so
+// it also finishes the dispatch (bucket offsets, sorted rows) that the
+// scan + scatter kernel does for larger T, saving that launch at decode sizes.
+template <int NP2, int SLOTS, int LPR, bool KFIX, bool RANK = false, bool SOLO = false>
 __global__ __launch_bounds__(256) void router_topk_kernel(const void* __restrict__ logits, int ldt, int64_t T, int E,
                                                           int k_rt, int norm, float* __restrict__ probs,
                                                           int64_t* __restrict__ idx_out, void* __restrict__ w_out,
                                                           int wdt, int32_t* __restrict__ rank_out,
-                                                          int32_t* __restrict__ counts_out) {
+                                                          int32_t* __restrict__ counts_out, DispatchOut dout) {
+  static_assert(!SOLO || RANK, "the single-block dispatch needs the rank step");
   static_assert(!RANK || SLOTS <= 8, "the fused rank step runs in the register (k <= 8) path");
   constexpr int C = NP2 / LPR;
   constexpr int RPB = 256 / LPR;  // rows per block
@@ -219,7 +232,9 @@ __global__ __launch_bounds__(256) void router_topk_kernel(const void* __restrict
       __shared__ uint32_t s_mask[(kRouterMaxExperts + 1) * (SBMAX / 32)];
       __shared__ uint32_t s_pref[(kRouterMaxExperts + 1) * (SBMAX / 32)];
       const int nbk = E + 1;
-      const int words = (RPB * k + 31) / 32;
+      // bitmask words for the slots of the rows this block holds (a single row at T = 1)
+      const int rows_here = (int)min((int64_t)RPB, T - (int64_t)blockIdx.x * RPB);
+      const int words = (rows_here * k + 31) / 32;
       for (int i = threadIdx.x; i < nbk * words; i += 256) s_mask[i] = 0u;
       __syncthreads();
 #pragma unroll
@@ -231,22 +246,57 @@ __global__ __launch_bounds__(256) void router_topk_kernel(const void* __restrict
         }
       }
       __syncthreads();
+      __shared__ int32_t s_off[kRouterMaxExperts + 1];
       for (int b = threadIdx.x; b < nbk; b += 256) {
         uint32_t run = 0;
         for (int w2 = 0; w2 < words; ++w2) {
           s_pref[b * words + w2] = run;
           run += __popc(s_mask[b * words + w2]);
         }
-        counts_out[(int64_t)blockIdx.x * nbk + b] = (int32_t)run;
+        if constexpr (SOLO) s_off[b] = (int32_t)run;
+        else counts_out[(int64_t)blockIdx.x * nbk + b] = (int32_t)run;
       }
       __syncthreads();
+      if constexpr (SOLO) {
+        // bucket totals -> exclusive offsets (wave 0), tokens_per_expert
+        if (threadIdx.x < 64) {
+          const int lane = threadIdx.x;
+          int32_t carry = 0;
+          for (int c = 0; c < nbk; c += 64) {
+            const int b = c + lane;
+            const int32_t v = b < nbk ? s_off[b] : 0;
+            int32_t incl = v;
+#pragma unroll
+            for (int o = 1; o < 64; o <<= 1) {
+              const int32_t u = __shfl_up(incl, o, 64);
+              if (lane >= o) incl += u;
+            }
+            if (b < nbk) {
+              if (b < E) dout.tokens_per_expert[b] = (int64_t)v;
+              s_off[b] = carry + incl - v;
+              dout.expert_offsets[b] = carry + incl - v;  // [E]: start of the out-of-range ids
+            }
+            carry += __shfl(incl, 63, 64);
+          }
+        }
+        __syncthreads();
+      }
 #pragma unroll
       for (int j = 0; j < SLOTS; ++j) {
         if (active && j < k && (j % LPR) == q) {
           const int ls = lr * k + j;
           const int b = (gi[j] >= 0 && gi[j] < E) ? gi[j] : E;
           const uint32_t below = s_mask[b * words + (ls >> 5)] & ((1u << (ls & 31)) - 1u);
-          rank_out[row * k + j] = (int32_t)(s_pref[b * words + (ls >> 5)] + __popc(below));
+          const int32_t rk = (int32_t)(s_pref[b * words + (ls >> 5)] + __popc(below));
+          if constexpr (SOLO) {
+            const int64_t sl = row * k + j;
+            const int32_t dst = s_off[b] + rk;
+            dout.sorted_token_idx[dst] = (int32_t)row;
+            if (dout.sort_idx) dout.sort_idx[dst] = sl;
+            dout.slot_to_row[sl] = dst;
+          } else {
+            rank_out[row * k + j] = rk;
+          }
         }
       }
     }
@@ -285,12 +335,19 @@ __global__ __launch_bounds__(256) void router_topk_kernel(const void* __restrict
 // Router with the fused rank step (k <= 8): RPB * k slots per rank block.
 template <int NP2>
 int launch_router_rank(const void* logits, int ldt, int64_t T, int E, int k, int norm, float* probs, int64_t* idx,
-                       void* w, int wdt, int32_t* rank, int32_t* counts, void* stream) {
+                       void* w, int wdt, int32_t* rank, int32_t* counts, const DispatchOut& dout, bool solo,
+                       void* stream) {
   constexpr int LPR = 4, RPB = 256 / LPR;
   dim3 grid((unsigned)((T + RPB - 1) / RPB)), block(256);
-#define HRM_RTR(SL, KF)                                                                                              \
-  HRM_LAUNCH((router_topk_kernel<NP2, SL, LPR, KF, true>), grid, block, 0, stream, logits, ldt, T, E, k, norm, probs, \
-             idx, w, wdt, rank, counts)
+#define HRM_RTR(SL, KF)                                                                                                \
+  do {                                                                                                                 \
+    if (solo)                                                                                                          \
+      HRM_LAUNCH((router_topk_kernel<NP2, SL, LPR, KF, true, true>), grid, block, 0, stream, logits, ldt, T, E, k,   \
+                 norm, probs, idx, w, wdt, rank, counts, dout);                                                        \
+    else                                                                                                               \
+      HRM_LAUNCH((router_topk_kernel<NP2, SL, LPR, KF, true>), grid, block, 0, stream, logits, ldt, T, E, k, norm,    \
+                 probs, idx, w, wdt, rank, counts, dout);                                                              \
+  } while (0)
   if (k == 2) HRM_RTR(2, true);
   else if (k == 4) HRM_RTR(4, true);
   else if (k == 8) HRM_RTR(8, true);
@@ -309,7 +366,7 @@ int launch_router_np2(const void* logits, int ldt, int64_t T, int E, int k, int 
   dim3 grid((unsigned)((T + RPB - 1) / RPB)), block(256);
 #define HRM_RT(SL, KF)                                                                                              \
   HRM_LAUNCH((router_topk_kernel<NP2, SL, LPR, KF>), grid, block, 0, stream, logits, ldt, T, E, k, norm, probs, idx, w, \
-             wdt, (int32_t*)nullptr, (int32_t*)nullptr)
+             wdt, (int32_t*)nullptr, (int32_t*)nullptr, DispatchOut{})
   if (k == 2) HRM_RT(2, true);
   else if (k == 4) HRM_RT(4, true);
   else if (k == 8) HRM_RT(8, true);
@@ -463,17 +520,21 @@ extern "C" int hrm_moe_router_topk_dispatch(const void* logits, int logits_dtype
   p += (sizeof(int32_t) * (size_t)R + 255) & ~size_t(255);
   int32_t* counts = reinterpret_cast<int32_t*>(p);
   if (num_tokens > 0) {
+    // up to 64 tokens: one router block finishes the dispatch itself (no second launch)
+    const bool solo = nb == 1;
+    const hrm::DispatchOut dout{tokens_per_expert, expert_offsets, sorted_token_idx, sort_idx, slot_to_row};
     int st;
     if (E <= 8)
       st = hrm::launch_router_rank<8>(logits, logits_dtype, num_tokens, E, k, norm_topk_prob, probs, topk_idx,
-                                      topk_weight, weight_dtype, rank, counts, stream);
+                                      topk_weight, weight_dtype, rank, counts, dout, solo, stream);
     else if (E <= 64)
       st = hrm::launch_router_rank<64>(logits, logits_dtype, num_tokens, E, k, norm_topk_prob, probs, topk_idx,
-                                       topk_weight, weight_dtype, rank, counts, stream);
+                                       topk_weight, weight_dtype, rank, counts, dout, solo, stream);
     else
       st = hrm::launch_router_rank<128>(logits, logits_dtype, num_tokens, E, k, norm_topk_prob, probs, topk_idx,
-                                        topk_weight, weight_dtype, rank, counts, stream);
+                                        topk_weight, weight_dtype, rank, counts, dout, solo, stream);
     if (st) return st;
+    if (solo) return HRM_MOE_OK;
   }
   return hrm::dispatch_from_ranks(topk_idx, R, E, k, 64 * k, nb, rank, counts, tokens_per_expert, expert_offsets,
                                   sorted_token_idx, sort_idx, slot_to_row, stream);
