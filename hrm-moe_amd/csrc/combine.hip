@@ -70,10 +70,12 @@ constexpr int kTokPerBlock = 8;
 constexpr int kBlock = 256;
 constexpr int kMaxTopK = 32;  // kTokPerBlock * kMaxTopK <= kBlock: one thread per routed slot
 
-// A block combines kTokPerBlock consecutive tokens.  Its threads first rank
-// each token's k rows (ascending row order is the summation order) into LDS,
-// then stride over (token, 16-byte chunk) items, so no lane idles when a
-// token's chunk count is not a multiple of the wave size.
+// A block combines kTokPerBlock consecutive tokens over one slice of the
+// columns (blockIdx.y of gridDim.y slices; one slice except at small T, where
+// the slices spread the loads of a few tokens over many CUs).  Its threads
+// first rank each token's k rows (ascending row order is the summation order)
+// into LDS, then stride over (token, 16-byte chunk) items, so no lane idles
+// when a token's chunk count is not a multiple of the wave size.
 // KU > 0: top-k fixed at compile time, so every row load of an item is issued
 // before the first product is added (all k loads in flight per lane).
 // KU == 0: any top-k up to kMaxTopK, rows loaded one after another.
@@ -112,11 +114,14 @@ __global__ __launch_bounds__(kBlock) void combine_kernel(const char* __restrict_
     s_w[tk][rank] = w;
   }
   __syncthreads();
-  const int chunks = (int)(H / P);
+  const int all_chunks = (int)(H / P);
+  const int per = (all_chunks + (int)gridDim.y - 1) / (int)gridDim.y;
+  const int c_lo = (int)blockIdx.y * per;
+  const int chunks = min(per, all_chunks - c_lo);  // this block's slice (may be empty)
   const int items = ntok * chunks;
   for (int it = tid; it < items; it += kBlock) {
     const int tk = it / chunks;
-    const int c = it - tk * chunks;
+    const int c = c_lo + (it - tk * chunks);
     float acc[P];
 #pragma unroll
     for (int q = 0; q < P; ++q) acc[q] = 0.0f;
@@ -292,7 +297,16 @@ extern "C" int hrm_moe_combine(const void* expert_out, const int32_t* slot_to_ro
   if (num_tokens == 0) return HRM_MOE_OK;
   if (!expert_out || !slot_to_row || !topk_weight || !expert_offsets || !out) return HRM_MOE_ERR_INVALID;
   if (hidden_size / 8 > (int64_t(1) << 27)) return HRM_MOE_ERR_UNSUPPORTED;  // items per block fit an int
-  dim3 grid((unsigned)((num_tokens + hrm::kTokPerBlock - 1) / hrm::kTokPerBlock)), block(hrm::kBlock);
+  // Column slices: enough for about 1024 blocks, but no more than one pass of
+  // the block's threads over its items needs (T = 8 at H = 1536: 6 slices, one
+  // load round each instead of six in one block).
+  const int64_t tok_blocks = (num_tokens + hrm::kTokPerBlock - 1) / hrm::kTokPerBlock;
+  const int64_t items = hrm::kTokPerBlock * (hidden_size / (dtype == HRM_MOE_F32 ? 4 : 8));
+  int64_t slices = (items + hrm::kBlock - 1) / hrm::kBlock;
+  const int64_t want = (1024 + tok_blocks - 1) / tok_blocks;
+  slices = slices < want ? slices : want;
+  slices = slices < 1 ? 1 : slices;
+  dim3 grid((unsigned)tok_blocks, (unsigned)slices), block(hrm::kBlock);
   const char* Y = static_cast<const char*>(expert_out);
   char* O = static_cast<char*>(out);
   if (dtype == HRM_MOE_BF16)
