@@ -654,8 +654,9 @@ __global__ __launch_bounds__(NW * 64, NW == 4 ? 2 : 1) void mgemm_dma_kernel(con
   static_assert(EPI == EPI_PLAIN || (EPI == EPI_SAVE_GU && KIND == KIND_GATHER_SWIGLU) ||
                     (EPI == EPI_SWIGLU_BWD && KIND == KIND_NN),
                 "epilogue mode does not fit the kernel kind");
-  constexpr int WGN = NW / 2;                                // waves along N (two along M)
-  constexpr int MB = BM / 64;                                // 32-row blocks per wave
+  constexpr int WGM = BM == 32 ? 1 : 2;                      // waves along M (32-row tiles: all along N)
+  constexpr int WGN = NW / WGM;                              // waves along N
+  constexpr int MB = BM / WGM / 32;                          // 32-row blocks per wave
   constexpr int NB = BN / WGN / 32;                          // 32-column blocks per wave
   constexpr int PK = BK * 2;                                 // bytes per K-contiguous tile row
   constexpr int LPRK = BK / 8;                               // DMA lanes per K-contiguous row
@@ -893,7 +894,7 @@ __global__ __launch_bounds__(NW * 64, NW == 4 ? 2 : 1) void mgemm_dma_kernel(con
   auto tile = [&](auto half_tag) __attribute__((always_inline)) {
     constexpr bool H = decltype(half_tag)::value;
     constexpr int MBH = H ? 2 : MB;                               // 32-row blocks per wave
-    const int row_base = H ? (wave >> 1) * 64 : wm * (BM / 2);    // first tile row of this wave
+    const int row_base = H ? (wave >> 1) * 64 : wm * (BM / WGM);  // first tile row of this wave
     const int col_blk = H ? (wave & 1) * 32 : wn * (BN / 2 / WGN);  // gate/up column block (gate/up kernel)
     floatx16 acc[NB][MBH];
 #pragma unroll
@@ -1607,9 +1608,10 @@ int launch_mgemm_dma(const void* A, const int32_t* gather, const void* W, const 
 // Tile shape, pipeline depth, waves and K step of the DMA kernels.
 // Default: 256 x 256 tiles with 8 waves (2 per SIMD, 128 x 64 per wave) and 2
 // stages of 64-wide K steps (128 KB of LDS) when experts average at least 256
-// rows and the weight rows split into whole 256-row tiles (not used for the
-// gate/up kernel by default; it supports a last half tile of 64 gate + 64 up
-// rows when selected explicitly); otherwise 128 x 128
+// rows and the weight rows split into whole 256-row tiles (the gate/up kernel
+// also supports a last half tile of 64 gate + 64 up rows when selected
+// explicitly); 32 x 256 tiles (4 waves along N, 4 stages, 144 KB) when
+// experts average at most 16 rows; otherwise 128 x 128
 // tiles, 4 waves, 2 stages (64 KB of LDS, two workgroups per CU).  The large
 // tile halves LDS and L2 traffic per flop; the small one wastes less on ragged
 // experts and on widths that are not multiples of 256.
@@ -1619,6 +1621,7 @@ struct MCfg {
   int bm, bn, stages, waves, bk;
 };
 bool mcfg_built(const MCfg& c) {
+  if (c.bm == 32) return c.bn == 256 && c.waves == 4 && c.bk == 64 && c.stages == 4;
   if (c.bm == 256 && c.bn == 128 && c.waves == 4) return c.bk == 32 && (c.stages == 2 || c.stages == 3);
   if (c.bm == 128 && c.bn == 128 && c.waves == 4)
     return (c.bk == 64 && (c.stages == 2 || c.stages == 3)) || (c.bk == 32 && (c.stages == 4 || c.stages == 5));
@@ -1644,6 +1647,12 @@ MCfg mgemm_cfg(int64_t M, int E, int64_t w_rows, bool gate_up, bool nn = false) 
   // than the idle columns of the last N tile.
   (void)gate_up;
   if (M >= (int64_t)E * 256 && (nn || w_rows % 256 == 0)) return MCfg{256, 256, 2, 8, 64};
+  // Decode sizes (experts average at most 16 rows): the GEMM streams weights,
+  // and 32-row tiles leave LDS for 4 stages of 256 weight rows (3 K steps in
+  // flight).  Decode layer at H = 1536, I = 512: T = 8 88.8 -> 82.8 us,
+  // T = 64 104.8 -> 100.8 us; at T = 256 (32 rows per expert) 128 x 128 stays
+  // faster (111.5 against 120.1 us).
+  if (!nn && M <= (int64_t)E * 16) return MCfg{32, 256, 4, 4, 64};
   return MCfg{128, 128, 2, 4, 64};
 }
 
@@ -1694,6 +1703,7 @@ int dispatch_mgemm_t(const void* A, const int32_t* gather, const void* W, const 
   }
 #define HRM_MG(BM_, BN_, ST_, NW_, BK_) \
   return launch_mgemm_dma<TR, KIND, BM_, BN_, ST_, NW_, BK_>(A, gather, W, tpe, M, N, K, E, a_rows, C, workspace, stream)
+  if (c.bm == 32) HRM_MG(32, 256, 4, 4, 64);
   if (c.bm == 256 && c.bn == 128) {
     if (c.stages == 2) HRM_MG(256, 128, 2, 4, 32);
     HRM_MG(256, 128, 3, 4, 32);
