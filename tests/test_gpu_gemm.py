@@ -6,7 +6,8 @@ in fp32 and rounds once, as the oracle does.  Only the summation order
 differs, so outputs agree to about one 16-bit ulp.  The bar: max |diff| <=
 1e-2 * max |ref| and mean |diff| <= 2e-3 * mean |ref|.  Cases cover ragged
 and empty experts, one expert holding every row, sizes that are not tile
-multiples, fp16, and the L / XL expert shapes.
+multiples, fp16, the L / XL expert shapes and decode sizes (at most 16 rows
+per expert on average, where the kernels take 32-row tiles).
 """
 import numpy as np
 import pytest
@@ -50,6 +51,9 @@ NT_CASES = [
     (20000, 1280, 448, 64, torch.bfloat16, "ragged"),
     (8192, 1024, 1536, 64, torch.bfloat16, "ragged"),
     (64, 896, 1280, 64, torch.bfloat16, "ragged"),
+    # decode sizes (32-row tiles): every row in one expert, and a ragged spread
+    (512, 1024, 1536, 64, torch.bfloat16, "one"),
+    (700, 320, 512, 64, torch.float16, "ragged"),
 ]
 
 

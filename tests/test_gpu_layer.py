@@ -51,6 +51,8 @@ LAYER_CASES = [
     ("decode_t8", 16, 8, 1536, 64, 512, 8, 0.0),
     ("decode_t64", 17, 64, 1536, 64, 512, 8, 0.0),
     ("decode_t256", 18, 256, 1536, 64, 512, 8, 0.0),
+    # L expert width at decode size: 32-row tiles with a partly used last gate/up N tile (I = 448)
+    ("l_decode_t16", 19, 16, 1280, 64, 448, 8, 0.0),
 ]
 
 
