@@ -100,7 +100,7 @@ __global__ __launch_bounds__(kBlock) void combine_kernel(const char* __restrict_
   float w = 0.0f;
   if (tid < nslot) {
     row = slot_to_row[t0 * k + tid];
-    w = El::weight(wts, t0 * k + tid);
+    w = wts ? El::weight(wts, t0 * k + tid) : 1.0f;  // no weights: the un-permute (round(y * 1) = y)
     s_raw[tid] = row;
   }
   __syncthreads();
@@ -295,7 +295,7 @@ extern "C" int hrm_moe_combine(const void* expert_out, const int32_t* slot_to_ro
   if (dtype < HRM_MOE_BF16 || dtype > HRM_MOE_F32) return HRM_MOE_ERR_DTYPE;
   if (top_k > hrm::kMaxTopK || hidden_size % 8) return HRM_MOE_ERR_UNSUPPORTED;
   if (num_tokens == 0) return HRM_MOE_OK;
-  if (!expert_out || !slot_to_row || !topk_weight || !expert_offsets || !out) return HRM_MOE_ERR_INVALID;
+  if (!expert_out || !slot_to_row || !expert_offsets || !out) return HRM_MOE_ERR_INVALID;  // weights may be NULL
   if (hidden_size / 8 > (int64_t(1) << 27)) return HRM_MOE_ERR_UNSUPPORTED;  // items per block fit an int
   // Column slices: enough for about 1024 blocks, but no more than one pass of
   // the block's threads over its items needs (T = 8 at H = 1536: 6 slices, one

@@ -131,6 +131,9 @@ class _RouterTopK(torch.autograd.Function):
         ctx.logits_dtype = logits.dtype
         extra = (d.tokens_per_expert, d.expert_offsets, d.sorted_token_idx, d.slot_to_row)
         ctx.mark_non_differentiable(idx, *extra)
+        # outputs without a gradient arrive as None, not as zero tensors that
+        # autograd would fill (five fill launches for the integer outputs)
+        ctx.set_materialize_grads(False)
         return (probs, w, idx) + extra
 
     @staticmethod
@@ -181,8 +184,7 @@ class _GroupedExpertsFn(torch.autograd.Function):
             d_gate_up = ops.down_dgrad_swiglu(d_rows, down_weight, tpe, gate_up)
             if need_h:
                 d_h_rows = ops.grouped_gemm_nn(d_gate_up, gate_up_weight, tpe)
-                ones = torch.ones_like(routing_weights)
-                d_h = ops.combine(d_h_rows, d, ones)
+                d_h = ops.combine(d_h_rows, d, None, top_k=routing_weights.shape[1])
             if need_gu:
                 d_gu_w = ops.grouped_gemm_tn_gather(d_gate_up, hidden, d.sorted_token_idx, tpe)
         return d_h, (d_w if need_w else None), d_gu_w, d_dn, None

@@ -309,16 +309,32 @@ def gate_up_swiglu(hidden: torch.Tensor, dispatch: Dispatch, gate_up_weight: tor
     return act
 
 
-def combine(expert_out: torch.Tensor, dispatch: Dispatch, topk_weight: torch.Tensor) -> torch.Tensor:
-    """out[t] = sum_j round(expert_out[row(t,j)] * w[t,j]) in fp32, rounded once; [T,H]."""
-    dev = _require_cuda(expert_out, topk_weight)
-    t, k = topk_weight.shape
-    r, h = expert_out.shape
-    if r != t * k:
-        raise ValueError(f"expert_out has {r} rows for {t} tokens x top-{k}")
-    if topk_weight.dtype != expert_out.dtype:
-        raise TypeError(f"dtype mismatch: expert_out {expert_out.dtype}, weights {topk_weight.dtype}")
-    expert_out, topk_weight = expert_out.contiguous(), topk_weight.contiguous()
+def combine(expert_out: torch.Tensor, dispatch: Dispatch, topk_weight: Optional[torch.Tensor],
+            top_k: Optional[int] = None) -> torch.Tensor:
+    """out[t] = sum_j round(expert_out[row(t,j)] * w[t,j]) in fp32, rounded once; [T,H].
+
+    ``topk_weight=None`` (then ``top_k`` is required) means unit weights: the
+    plain sum of each token's rows, as the layer's backward un-permutes d(hidden).
+    """
+    if topk_weight is None:
+        if top_k is None:
+            raise ValueError("combine without weights needs top_k")
+        dev = _require_cuda(expert_out)
+        k = int(top_k)
+        r, h = expert_out.shape
+        if k < 1 or r % k:
+            raise ValueError(f"expert_out has {r} rows, not a multiple of top-{k}")
+        t = r // k
+    else:
+        dev = _require_cuda(expert_out, topk_weight)
+        t, k = topk_weight.shape
+        r, h = expert_out.shape
+        if r != t * k:
+            raise ValueError(f"expert_out has {r} rows for {t} tokens x top-{k}")
+        if topk_weight.dtype != expert_out.dtype:
+            raise TypeError(f"dtype mismatch: expert_out {expert_out.dtype}, weights {topk_weight.dtype}")
+        topk_weight = topk_weight.contiguous()
+    expert_out = expert_out.contiguous()
     e = dispatch.tokens_per_expert.numel()
     out = expert_out.new_empty((t, h))
     with _lib.device_guard(dev):

@@ -158,6 +158,8 @@ int hrm_moe_gate_up_swiglu(const void* hidden, const int32_t* sorted_token_idx, 
  * index_add_ compute on the CPU (models/layers.py:333-334).  Slots whose row
  * is >= expert_offsets[E] (dropped expert ids) contribute nothing.
  *   expert_out [R,H], topk_weight [T,k], out [T,H]; dtype bf16, f16 or f32.
+ * topk_weight may be NULL: every weight is 1, the un-permute of the layer's
+ * backward (sum of each token's rows, same order and single rounding).
  * Limits: H a multiple of 8, 1 <= k <= 32.
  */
 int hrm_moe_combine(const void* expert_out, const int32_t* slot_to_row, const void* topk_weight,

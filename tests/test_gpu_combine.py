@@ -45,3 +45,17 @@ def test_combine_bit_exact(cuda, t, h, e, k, dtype):
     ref = mo.combine(y, sorted_w, perm["sorted_token_idx"], t)
     assert out.dtype == dtype and out.shape == (t, h)
     assert torch.equal(out.cpu(), ref)
+
+
+@pytest.mark.parametrize("t,h,e,k,dtype", [(13, 1280, 64, 8, torch.bfloat16), (45, 520, 32, 5, torch.float16),
+                                           (64, 384, 8, 2, torch.float32)])
+def test_combine_unit_weights(cuda, t, h, e, k, dtype):
+    """No weight tensor: the plain sum of each token's rows (the backward's un-permute), checked
+    against the oracle's combine with weights of one."""
+    idx = _distinct_topk(t * 5 + k, t, e, k)
+    d = ops.permute(torch.from_numpy(idx).to(cuda), e)
+    perm = mo.permute(idx, e)
+    y = torch.from_numpy(synth.normal(t + h + 1, (t * k, h))).to(dtype)
+    out = ops.combine(y.to(cuda), d, None, top_k=k)
+    ref = mo.combine(y, torch.ones(t * k, dtype=dtype), perm["sorted_token_idx"], t)
+    assert torch.equal(out.cpu(), ref)
