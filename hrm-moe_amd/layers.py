@@ -80,11 +80,25 @@ def load_balancing_loss_func(routing_weights: Tensor, selected_experts: Tensor, 
     return torch.sum(tokens_per_expert * router_prob_per_expert) * num_experts
 
 
+_ONE_GROUP: dict = {}
+
+
+def _one_group_counts(rows: int, device: torch.device) -> Tensor:
+    """tokens_per_expert = [rows] on the device, cached so the backward launches no copy for it."""
+    key = (rows, device)
+    t = _ONE_GROUP.get(key)
+    if t is None:
+        if len(_ONE_GROUP) > 64:
+            _ONE_GROUP.clear()
+        t = _ONE_GROUP[key] = torch.tensor([rows], dtype=torch.int64, device=device)
+    return t
+
+
 class _GateLinear(torch.autograd.Function):
     """The router gate ``F.linear(h, W)`` (models/layers.py:605, :89-90) with a HIP weight gradient.
 
     Forward is the same F.linear call, so the logits are the same bits.  The
-    backward's input grad is ``dlogits @ W``; the weight grad ``dlogits^T @ h``
+    backward's input grad is ``dlogits @ W`` (a one-group HIP grouped GEMM); the weight grad ``dlogits^T @ h``
     (one long reduction over the tokens into a small [E,H] output) runs as a
     split-K HIP kernel with fp32 partials.
     """
@@ -97,8 +111,13 @@ class _GateLinear(torch.autograd.Function):
     @staticmethod
     def backward(ctx, grad_logits: Tensor):
         hidden, weight = ctx.saved_tensors
-        grad_logits = grad_logits.to(hidden.dtype)
-        d_hidden = grad_logits @ weight if ctx.needs_input_grad[0] else None
+        grad_logits = grad_logits.to(hidden.dtype).contiguous()
+        d_hidden = None
+        if ctx.needs_input_grad[0]:
+            # dlogits [T,E] . W [E,H] as a one-group NN grouped GEMM (K = E): at T = 16384,
+            # E = 64, H = 1280 it takes 15 us against 26 us for the hipBLASLt matmul
+            t = grad_logits.shape[0]
+            d_hidden = ops.grouped_gemm_nn(grad_logits, weight.unsqueeze(0), _one_group_counts(t, hidden.device))
         d_weight = None
         if ctx.needs_input_grad[1]:
             d_weight = ops.gate_wgrad(grad_logits, hidden).to(weight.dtype)
