@@ -55,8 +55,11 @@ PROTOTYPES = {
                                             _P, _SZ, _P]),
     "hrm_moe_gate_wgrad_workspace_size": (_SZ, [_I64, _I32, _I64]),
     "hrm_moe_gate_wgrad": (_INT, [_P, _P, _I64, _I32, _I64, _INT, _P, _P, _SZ, _P]),
-    "hrm_moe_router_topk_backward": (_INT, [_P, _P, _P, _INT, _P, _I64, _I32, _I32, _I32, _P, _INT, _P]),
+    "hrm_moe_router_topk_backward": (_INT, [_P, _P, _P, _INT, _P, _I64, _I64, _I32, _I32, _I32, _P, _INT, _P]),
     "hrm_moe_grouped_gemm_tn_gather": (_INT, [_P, _P, _P, _I64, _P, _I64, _I64, _I64, _I32, _INT, _P, _P, _SZ, _P]),
+    "hrm_moe_aux_loss_workspace_size": (_SZ, [_I64, _I32]),
+    "hrm_moe_aux_loss": (_INT, [_P, _I64, _I32, _P, _P, _P, _P, _P, _SZ, _P]),
+    "hrm_moe_aux_loss_backward": (_INT, [_P, _P, _I64, _I32, _P, _P]),
 }
 
 _lock = threading.Lock()

@@ -397,7 +397,8 @@ int launch_router_np2(const void* logits, int ldt, int64_t T, int E, int k, int 
 constexpr int kBwdTokPerBlock = 4;
 __global__ __launch_bounds__(kBwdTokPerBlock * 64) void router_bwd_kernel(
     const float* __restrict__ probs, const int64_t* __restrict__ idx, const void* __restrict__ g_w, int gw_dt,
-    const float* __restrict__ g_probs, int64_t T, int E, int k, int norm, void* __restrict__ dlogits, int out_dt) {
+    const float* __restrict__ g_probs, int64_t gp_stride, int64_t T, int E, int k, int norm, void* __restrict__ dlogits,
+    int out_dt) {
   const int lane = threadIdx.x & 63;
   const int64_t t = (int64_t)blockIdx.x * kBwdTokPerBlock + (threadIdx.x >> 6);
   if (t >= T) return;  // no barriers below
@@ -426,7 +427,7 @@ __global__ __launch_bounds__(kBwdTokPerBlock * 64) void router_bwd_kernel(
   for (int h = 0; h < 2; ++h) {
     const int e = lane + 64 * h;
     p[h] = e < E ? prow[e] : 0.0f;
-    dp[h] = (e < E && g_probs) ? g_probs[t * E + e] : 0.0f;
+    dp[h] = (e < E && g_probs) ? g_probs[t * gp_stride + e] : 0.0f;  // stride 0: one row for all tokens
   }
   for (int j = 0; j < k; ++j) {
     const int e = __shfl(ej, j, 64);
@@ -461,10 +462,12 @@ extern "C" int hrm_moe_router_topk(const void* logits, int logits_dtype, int64_t
 }
 
 extern "C" int hrm_moe_router_topk_backward(const float* probs, const int64_t* topk_idx, const void* grad_weight,
-                                            int grad_weight_dtype, const float* grad_probs, int64_t num_tokens,
+                                            int grad_weight_dtype, const float* grad_probs,
+                                            int64_t grad_probs_row_stride, int64_t num_tokens,
                                             int32_t num_experts, int32_t top_k, int32_t norm_topk_prob,
                                             void* grad_logits, int logits_dtype, void* stream) {
   if (num_tokens < 0 || num_experts < 1 || top_k < 1 || top_k > num_experts) return HRM_MOE_ERR_INVALID;
+  if (grad_probs && grad_probs_row_stride != 0 && grad_probs_row_stride < num_experts) return HRM_MOE_ERR_INVALID;
   if (grad_weight_dtype < HRM_MOE_BF16 || grad_weight_dtype > HRM_MOE_F32) return HRM_MOE_ERR_DTYPE;
   if (logits_dtype < HRM_MOE_BF16 || logits_dtype > HRM_MOE_F32) return HRM_MOE_ERR_DTYPE;
   if (num_experts > 128 || top_k > 32) return HRM_MOE_ERR_UNSUPPORTED;
@@ -472,7 +475,8 @@ extern "C" int hrm_moe_router_topk_backward(const float* probs, const int64_t* t
   if (!probs || !topk_idx || !grad_weight || !grad_logits) return HRM_MOE_ERR_INVALID;
   const dim3 grid((unsigned)((num_tokens + hrm::kBwdTokPerBlock - 1) / hrm::kBwdTokPerBlock));
   hipLaunchKernelGGL(hrm::router_bwd_kernel, grid, dim3(hrm::kBwdTokPerBlock * 64), 0, (hipStream_t)stream, probs,
-                     topk_idx, grad_weight, grad_weight_dtype, grad_probs, num_tokens, num_experts, top_k,
+                     topk_idx, grad_weight, grad_weight_dtype, grad_probs, grad_probs_row_stride, num_tokens,
+                     num_experts, top_k,
                      norm_topk_prob, grad_logits, logits_dtype);
   const hipError_t err = hipGetLastError();
   return err == hipSuccess ? HRM_MOE_OK : (int)err;

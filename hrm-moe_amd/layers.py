@@ -165,6 +165,32 @@ class _RouterTopK(torch.autograd.Function):
         return dz, None, None, None
 
 
+class _AuxLoss(torch.autograd.Function):
+    """load_balancing_loss_func and the expert counts as two HIP launches (models/layers.py:163-170, :619-632).
+
+    The loss's gradient is the same row for every token, ((g * E) * f[e]) * (1 / T);
+    it is returned as a stride-0 view, which the router backward reads as one
+    row instead of a [T,E] tensor.
+    """
+
+    @staticmethod
+    def forward(ctx, probs: Tensor, tokens_per_expert: Tensor):
+        aux, counts, frac = ops.aux_loss(probs, tokens_per_expert)
+        ctx.save_for_backward(frac)
+        ctx.num_tokens = probs.shape[0]
+        ctx.mark_non_differentiable(counts)
+        ctx.set_materialize_grads(False)
+        return aux, counts
+
+    @staticmethod
+    def backward(ctx, g_aux, _g_counts):
+        if g_aux is None:
+            return None, None
+        (frac,) = ctx.saved_tensors
+        row = ops.aux_loss_backward(g_aux, frac, ctx.num_tokens)
+        return row.unsqueeze(0).expand(ctx.num_tokens, row.numel()), None
+
+
 class _GroupedExpertsFn(torch.autograd.Function):
     """Grouped expert block (models/layers.py:317-334) with a HIP backward.
 
@@ -394,12 +420,19 @@ class SparseMoESwiGLU(nn.Module):
                 aux_selected_experts = aux_selected_experts[:valid_tokens]
                 counts = None
             with record_moe_profile_phase("aux_metrics"):
-                aux_loss = load_balancing_loss_func(aux_routing_probs, aux_selected_experts, self.num_experts,
-                                                    tokens_per_expert=counts)
-                moe_context.setdefault("aux_losses", []).append(aux_loss)
-                with torch.no_grad():
-                    if counts is None:
-                        counts = torch.bincount(aux_selected_experts.reshape(-1), minlength=self.num_experts)
-                    moe_context.setdefault("expert_counts", []).append(counts.to(torch.float32))
+                if (counts is not None and aux_routing_probs.is_cuda and aux_routing_probs.dtype == torch.float32
+                        and aux_routing_probs.shape[0] > 0 and self.num_experts <= 1024):
+                    # loss and counts in two launches instead of torch's chain of small kernels
+                    aux_loss, counts_f = _AuxLoss.apply(aux_routing_probs, counts)
+                    moe_context.setdefault("aux_losses", []).append(aux_loss)
+                    moe_context.setdefault("expert_counts", []).append(counts_f)
+                else:
+                    aux_loss = load_balancing_loss_func(aux_routing_probs, aux_selected_experts, self.num_experts,
+                                                        tokens_per_expert=counts)
+                    moe_context.setdefault("aux_losses", []).append(aux_loss)
+                    with torch.no_grad():
+                        if counts is None:
+                            counts = torch.bincount(aux_selected_experts.reshape(-1), minlength=self.num_experts)
+                        moe_context.setdefault("expert_counts", []).append(counts.to(torch.float32))
 
         return final_hidden_states.reshape(original_shape)

@@ -90,15 +90,63 @@ def router_topk_backward(probs: torch.Tensor, topk_idx: torch.Tensor, grad_weigh
     probs = probs.contiguous()
     topk_idx = topk_idx.to(torch.int64).contiguous()
     grad_weight = grad_weight.contiguous()
-    grad_probs = grad_probs.contiguous() if grad_probs is not None else None
+    gp_stride = e
+    if grad_probs is not None:
+        if grad_probs.shape != (t, e):
+            raise ValueError(f"grad_probs has shape {tuple(grad_probs.shape)}, expected {(t, e)}")
+        if grad_probs.stride() == (0, 1):
+            gp_stride = 0  # one row broadcast over the tokens (e.g. the auxiliary loss's gradient): not copied
+        else:
+            grad_probs = grad_probs.contiguous()
     out = torch.empty((t, e), dtype=logits_dtype, device=dev)
     with _lib.device_guard(dev):
         st = _lib.lib().hrm_moe_router_topk_backward(
             _lib.ptr(probs), _lib.ptr(topk_idx), _lib.ptr(grad_weight), _lib.dtype_code(grad_weight.dtype),
-            _lib.ptr(grad_probs), t, e, k, int(bool(norm_topk_prob)), _lib.ptr(out), _lib.dtype_code(logits_dtype),
-            _lib.stream_of(dev))
+            _lib.ptr(grad_probs), gp_stride, t, e, k, int(bool(norm_topk_prob)), _lib.ptr(out),
+            _lib.dtype_code(logits_dtype), _lib.stream_of(dev))
     _lib.check(st, "router_topk_backward")
     return out
+
+
+def aux_loss(probs: torch.Tensor, tokens_per_expert: torch.Tensor):
+    """(aux [] fp32, expert_counts [E] fp32, expert_fraction [E] fp32) of the load-balancing loss.
+
+    aux = (sum_e (tpe[e] / T) * mean_t probs[t, e]) * E (models/layers.py:163-170), in two
+    launches with a fixed summation order.
+    """
+    dev = _require_cuda(probs, tokens_per_expert)
+    if probs.dim() != 2 or probs.dtype != torch.float32:
+        raise TypeError("aux_loss needs fp32 probabilities [tokens, experts]")
+    t, e = probs.shape
+    if t < 1:
+        raise ValueError("aux_loss needs at least one token")
+    probs = probs.contiguous()
+    tpe = _tpe64(tokens_per_expert, dev)
+    if tpe.numel() != e:
+        raise ValueError(f"tokens_per_expert has {tpe.numel()} entries for {e} experts")
+    aux = torch.empty((), dtype=torch.float32, device=dev)
+    counts = torch.empty(e, dtype=torch.float32, device=dev)
+    frac = torch.empty(e, dtype=torch.float32, device=dev)
+    lib = _lib.lib()
+    ws = _workspace(lib.hrm_moe_aux_loss_workspace_size(t, e), dev)
+    with _lib.device_guard(dev):
+        st = lib.hrm_moe_aux_loss(_lib.ptr(probs), t, e, _lib.ptr(tpe), _lib.ptr(aux), _lib.ptr(counts),
+                                  _lib.ptr(frac), _lib.ptr(ws), ws.numel(), _lib.stream_of(dev))
+    _lib.check(st, "aux_loss")
+    return aux, counts, frac
+
+
+def aux_loss_backward(grad_aux: torch.Tensor, expert_fraction: torch.Tensor, num_tokens: int) -> torch.Tensor:
+    """d aux / d probs[t, e] for every token: the row ((g * E) * f[e]) * (1 / T), [E] fp32."""
+    dev = _require_cuda(grad_aux, expert_fraction)
+    grad_aux = grad_aux.to(torch.float32).contiguous()
+    e = expert_fraction.numel()
+    row = torch.empty(e, dtype=torch.float32, device=dev)
+    with _lib.device_guard(dev):
+        st = _lib.lib().hrm_moe_aux_loss_backward(_lib.ptr(grad_aux), _lib.ptr(expert_fraction), int(num_tokens), e,
+                                                  _lib.ptr(row), _lib.stream_of(dev))
+    _lib.check(st, "aux_loss_backward")
+    return row
 
 
 # ---------------------------------------------------------------------------

@@ -214,11 +214,14 @@ int hrm_moe_combine_backward(const void* grad_out, const void* expert_out, const
  *   dp[t,e] = grad_probs[t,e] + sum over j with idx_j = e of dv_j
  *   grad_logits[t,e] = probs[t,e] * (dp[t,e] - sum_e' probs[t,e'] dp[t,e'])
  * probs [T,E] fp32 (the forward's output), topk_idx [T,k] int64, grad_weight
- * [T,k], grad_probs [T,E] fp32 or NULL (no gradient reaches the
- * probabilities), grad_logits [T,E] in logits_dtype.  Deterministic.
- * Limits: E <= 128, k <= 32. */
+ * [T,k], grad_probs fp32 or NULL (no gradient reaches the probabilities):
+ * row t at grad_probs + t * grad_probs_row_stride, the stride E for a [T,E]
+ * tensor or 0 for one row shared by every token (the auxiliary loss's gradient,
+ * which is the same for all tokens).  grad_logits [T,E] in logits_dtype.
+ * Deterministic.  Limits: E <= 128, k <= 32. */
 int hrm_moe_router_topk_backward(const float* probs, const int64_t* topk_idx, const void* grad_weight,
-                                 int grad_weight_dtype, const float* grad_probs, int64_t num_tokens,
+                                 int grad_weight_dtype, const float* grad_probs, int64_t grad_probs_row_stride,
+                                 int64_t num_tokens,
                                  int32_t num_experts, int32_t top_k, int32_t norm_topk_prob, void* grad_logits,
                                  int logits_dtype, void* stream);
 
@@ -244,6 +247,25 @@ int hrm_moe_grouped_gemm_tn_gather(const void* A, const void* B, const int32_t* 
                                    const int64_t* tokens_per_expert, int64_t M, int64_t Na, int64_t Nb,
                                    int32_t num_experts, int dtype, void* C, void* workspace, size_t workspace_bytes,
                                    void* stream);
+
+/*
+ * Auxiliary load-balancing loss and expert counts of the layer
+ * (models/layers.py:163-170 load_balancing_loss_func, :619-632 counts):
+ *   f[e] = tokens_per_expert[e] * (1/T),  mean[e] = sum_t probs[t,e] * (1/T)
+ *   aux_loss[0] = (sum_e f[e] * mean[e]) * E,  expert_counts[e] = tokens_per_expert[e]
+ * and expert_fraction[e] = f[e] for the backward.  probs [T,E] fp32 (the
+ * router's), tokens_per_expert [E] int64 (the dispatch's counts, equal to
+ * the reference's bincount).  Sums run in a fixed order (deterministic).
+ * Workspace: hrm_moe_aux_loss_workspace_size.  Limits: T >= 1, E <= 1024.
+ */
+size_t hrm_moe_aux_loss_workspace_size(int64_t num_tokens, int32_t num_experts);
+int hrm_moe_aux_loss(const float* probs, int64_t num_tokens, int32_t num_experts, const int64_t* tokens_per_expert,
+                     float* aux_loss, float* expert_counts, float* expert_fraction, void* workspace,
+                     size_t workspace_bytes, void* stream);
+/* Its gradient, the same for every token: grad_probs_row[e] = ((grad_aux[0] * E) * f[e]) * (1/T),
+ * to pass to hrm_moe_router_topk_backward with grad_probs_row_stride = 0. */
+int hrm_moe_aux_loss_backward(const float* grad_aux, const float* expert_fraction, int64_t num_tokens,
+                              int32_t num_experts, float* grad_probs_row, void* stream);
 
 #ifdef __cplusplus
 }

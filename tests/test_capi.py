@@ -124,11 +124,22 @@ def test_training_entry_points_reject_bad_arguments():
     assert rd(buf, 7, 16, 64, 8, 1, buf, buf, buf, _lib.BF16, buf, buf, buf, NULL, buf, buf, rws,
               NULL) == _lib.ERR_DTYPE
     rb = lib.hrm_moe_router_topk_backward
-    assert rb(buf, buf, buf, _lib.BF16, NULL, 16, 200, 8, 1, buf, _lib.BF16, NULL) == _lib.ERR_UNSUPPORTED
-    assert rb(buf, buf, buf, 9, NULL, 16, 64, 8, 1, buf, _lib.BF16, NULL) == _lib.ERR_DTYPE
-    assert rb(buf, buf, buf, _lib.BF16, NULL, 16, 64, 65, 1, buf, _lib.BF16, NULL) == _lib.ERR_INVALID
-    assert rb(buf, NULL, buf, _lib.BF16, NULL, 16, 64, 8, 1, buf, _lib.BF16, NULL) == _lib.ERR_INVALID
-    assert rb(buf, buf, buf, _lib.BF16, NULL, 0, 64, 8, 1, buf, _lib.BF16, NULL) == _lib.OK
+    assert rb(buf, buf, buf, _lib.BF16, NULL, 0, 16, 200, 8, 1, buf, _lib.BF16, NULL) == _lib.ERR_UNSUPPORTED
+    assert rb(buf, buf, buf, 9, NULL, 0, 16, 64, 8, 1, buf, _lib.BF16, NULL) == _lib.ERR_DTYPE
+    assert rb(buf, buf, buf, _lib.BF16, NULL, 0, 16, 64, 65, 1, buf, _lib.BF16, NULL) == _lib.ERR_INVALID
+    assert rb(buf, NULL, buf, _lib.BF16, NULL, 0, 16, 64, 8, 1, buf, _lib.BF16, NULL) == _lib.ERR_INVALID
+    assert rb(buf, buf, buf, _lib.BF16, buf, 32, 16, 64, 8, 1, buf, _lib.BF16, NULL) == _lib.ERR_INVALID  # stride < E
+    assert rb(buf, buf, buf, _lib.BF16, NULL, 0, 0, 64, 8, 1, buf, _lib.BF16, NULL) == _lib.OK
+    aw = lib.hrm_moe_aux_loss_workspace_size(16384, 64)
+    assert aw >= 64 * 4 and lib.hrm_moe_aux_loss_workspace_size(0, 64) == 0
+    al = lib.hrm_moe_aux_loss
+    assert al(buf, 16384, 64, buf, buf, buf, buf, buf, aw - 1, NULL) == _lib.ERR_WORKSPACE
+    assert al(buf, 16384, 2000, buf, buf, buf, buf, buf, aw, NULL) == _lib.ERR_UNSUPPORTED
+    assert al(buf, 0, 64, buf, buf, buf, buf, buf, aw, NULL) == _lib.ERR_INVALID
+    assert al(buf, 16384, 64, NULL, buf, buf, buf, buf, aw, NULL) == _lib.ERR_INVALID
+    ab = lib.hrm_moe_aux_loss_backward
+    assert ab(NULL, buf, 16384, 64, buf, NULL) == _lib.ERR_INVALID
+    assert ab(buf, buf, 0, 64, buf, NULL) == _lib.ERR_INVALID
     tg = lib.hrm_moe_grouped_gemm_tn_gather
     assert tg(buf, buf, buf, 100, buf, 1024, 256, 252, 64, _lib.BF16, buf, buf, ws, NULL) == _lib.ERR_UNSUPPORTED
     assert tg(buf, buf, NULL, 100, buf, 1024, 256, 256, 64, _lib.BF16, buf, buf, ws, NULL) == _lib.ERR_INVALID

@@ -124,6 +124,22 @@ def test_router_backward_matches_oracle(cuda, t, e, k, norm, with_gp):
     assert torch.equal(got, again)
 
 
+@pytest.mark.parametrize("t,e,k", [(1000, 64, 8), (300, 128, 4)])
+def test_router_backward_broadcast_prob_grad(cuda, t, e, k):
+    """A probability gradient that is one row for every token (stride 0, as the auxiliary loss's)
+    gives the bits of the same gradient materialised as a [T,E] tensor."""
+    from oracle import synth
+    logits = torch.from_numpy(synth.normal(t + 5, (t, e))).to(torch.bfloat16).to(cuda)
+    probs, _, idx = ops.router_topk(logits, k, True, torch.bfloat16)
+    gw = torch.from_numpy(synth.normal(t + 6, (t, k))).to(torch.bfloat16).to(cuda)
+    row = torch.from_numpy(synth.normal(t + 7, (e,), std=0.01)).to(cuda)
+    bcast = row.unsqueeze(0).expand(t, e)
+    assert bcast.stride() == (0, 1)
+    got = ops.router_topk_backward(probs, idx, gw, bcast, True, torch.bfloat16)
+    want = ops.router_topk_backward(probs, idx, gw, bcast.contiguous(), True, torch.bfloat16)
+    assert torch.equal(got, want)
+
+
 @pytest.mark.parametrize("t,e,h", [(16384, 64, 1280), (512, 8, 256), (1000, 128, 1536), (100, 16, 264),
                                    (40000, 64, 1536)])
 def test_gate_wgrad_matches_fp32_product(cuda, t, e, h):
