@@ -314,7 +314,10 @@ int dispatch_from_ranks(const int64_t* topk_idx, int64_t R, int E, int k, int SB
                         const int32_t* counts, int64_t* tokens_per_expert, int32_t* expert_offsets,
                         int32_t* sorted_token_idx, int64_t* sort_idx, int32_t* slot_to_row, void* stream) {
   if (E + 1 > 512) return HRM_MOE_ERR_UNSUPPORTED;
-  const int G = nb <= 32 ? 1 : (nb + 31) / 32;
+  // about 256 workgroups: each re-reads the whole counts matrix for its prefix,
+  // but more of them scatter in parallel (L: 9.5 -> 6.2 us against 32 workgroups;
+  // T = 32768, E = 128: 17.6 -> 10.4 us)
+  const int G = nb <= 256 ? 1 : (nb + 255) / 256;
   const int blocks = nb == 0 ? 1 : (nb + G - 1) / G;
   HRM_LAUNCH(permute_scan_scatter_kernel, dim3(blocks), dim3(1024), 0, stream, topk_idx, R, E, k, SB, nb, G, rank,
              counts, tokens_per_expert, expert_offsets, sorted_token_idx, sort_idx, slot_to_row);
