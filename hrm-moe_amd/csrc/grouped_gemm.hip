@@ -555,8 +555,9 @@ __global__ __launch_bounds__(256) void sum_splits_kernel(const float* __restrict
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
 }
+template <int CPOL = 0>
 __device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t r, char* lds_dst, uint32_t voff, uint32_t soff) {
-  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (HRM_LDS void*)lds_dst, 16, voff, soff, 0, 0);
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (HRM_LDS void*)lds_dst, 16, voff, soff, 0, CPOL);
 }
 template <int N>
 __device__ __forceinline__ void wait_vmcnt() {
@@ -619,16 +620,16 @@ __device__ __forceinline__ u32x4 bload16(__amdgpu_buffer_rsrc_t r, uint32_t voff
   return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, voff, 0, 0));
 }
 
-// Non-temporal (nt) policy for stores of output that nothing re-reads from L2
-// soon.  The persistent kernels' first wait of the next tile also waits for
+// Non-temporal (nt) cache policy bit, for stores of output that nothing
+// re-reads from L2 soon (and for the weight loads of the decode-size tiles).  The persistent kernels' first wait of the next tile also waits for
 // the previous tile's stores, and nt stores are acknowledged sooner: the NT
 // GEMM at L (131072 x 1280 x 448) measured 177 against 204 us, and the L
 // training step (dgrad and wgrad outputs too) 2384 against 2398 us.
-constexpr int kStoreNT = 2;
+constexpr int kCpolNT = 2;
 __device__ __forceinline__ void bstore8(__amdgpu_buffer_rsrc_t r, uint32_t voff, u32x2 v) {
   __builtin_amdgcn_raw_buffer_store_b64(v, r, voff, 0, 0);
 }
-// CPOL: cache policy bits of the store (0, or kStoreNT)
+// CPOL: cache policy bits of the store (0, or kCpolNT)
 template <int CPOL = 0>
 __device__ __forceinline__ void bstore16(__amdgpu_buffer_rsrc_t r, uint32_t voff, u32x4 v) {
   __builtin_amdgcn_raw_buffer_store_b128(v, r, voff, 0, CPOL);
@@ -865,8 +866,12 @@ __global__ __launch_bounds__(NW * 64, NW == 4 ? 2 : 1) void mgemm_dma_kernel(con
 #pragma unroll
       for (int i = 0; i < B_INSTR; ++i) dma16(rB, sb + (wave * NN_KR + i * NN_RPI) * (BN * 2), b_off[i], kb);
     } else {
+      // 32-row tiles run at decode sizes, where each expert's weight rows are
+      // read once: non-temporal loads (decode layer T = 8 82.9 -> 73.8 us,
+      // T = 64 99.4 -> 88.3 us).  Larger tiles re-read them from L2 across M tiles.
+      constexpr int BPOL = BM == 32 ? kCpolNT : 0;
 #pragma unroll
-      for (int i = 0; i < B_INSTR; ++i) dma16(rB, sb + (wave * B_ROWS + i * RPIK) * PK, b_off[i], ka);
+      for (int i = 0; i < B_INSTR; ++i) dma16<BPOL>(rB, sb + (wave * B_ROWS + i * RPIK) * PK, b_off[i], ka);
     }
     ++iss_step;
     ++issued;
@@ -1043,7 +1048,7 @@ __global__ __launch_bounds__(NW * 64, NW == 4 ? 2 : 1) void mgemm_dma_kernel(con
             // the down projection's rows (and dgrad's d(hidden) rows) go to the combine /
             // un-permute, which reads them from HBM; the gate/up kernel's act rows
             // are re-read by the down GEMM right away
-            bstore16<(KIND == KIND_NT || KIND == KIND_NN) ? kStoreNT : 0>(rC, voff, v);
+            bstore16<(KIND == KIND_NT || KIND == KIND_NN) ? kCpolNT : 0>(rC, voff, v);
           } else {
             // EPI_SAVE_GU: gate to columns [0, N), up to [N, 2N) of aux
             const uint32_t xoff =
@@ -1391,7 +1396,7 @@ __global__ __launch_bounds__(NW * 64, 1) void wgrad_dma8_kernel(const uint16_t* 
           const uint32_t ml = (uint32_t)(wm * (BA / 2) + p0 * 32 + r);
           const int c = col0 + c16 * 8;
           const uint32_t voff = c < Nb ? (ml * (uint32_t)Nb + (uint32_t)c) * 2 : 0x80000000u;
-          bstore16<kStoreNT>(rC, voff, v);  // weight gradients: written once, read by the optimizer
+          bstore16<kCpolNT>(rC, voff, v);  // weight gradients: written once, read by the optimizer
         }
       }
     }
