@@ -644,7 +644,9 @@ __device__ __forceinline__ void bstore16(__amdgpu_buffer_rsrc_t r, uint32_t voff
 // stores and no branch is taken.
 // 4-wave variants are sized for two workgroups per CU (at most 256 registers
 // per lane, two waves per SIMD); 8-wave variants run one per CU.
-template <typename TR, int KIND, int BM, int BN, int STAGES, int NW, int BK, int EPI = EPI_PLAIN>
+// WNT: weight rows are loaded non-temporally (each expert's weights are read
+// by about one M tile: decode and mid-size token counts).
+template <typename TR, int KIND, int BM, int BN, int STAGES, int NW, int BK, int EPI = EPI_PLAIN, bool WNT = false>
 __global__ __launch_bounds__(NW * 64, NW == 4 ? 2 : 1) void mgemm_dma_kernel(const uint16_t* __restrict__ A,
                                                                const int32_t* __restrict__ gather,
                                                                const uint16_t* __restrict__ W,
@@ -868,8 +870,9 @@ __global__ __launch_bounds__(NW * 64, NW == 4 ? 2 : 1) void mgemm_dma_kernel(con
     } else {
       // 32-row tiles run at decode sizes, where each expert's weight rows are
       // read once: non-temporal loads (decode layer T = 8 82.9 -> 73.8 us,
-      // T = 64 99.4 -> 88.3 us).  Larger tiles re-read them from L2 across M tiles.
-      constexpr int BPOL = BM == 32 ? kCpolNT : 0;
+      // T = 64 99.4 -> 88.3 us).  Larger tiles re-read them from L2 across M
+      // tiles, except with few rows per expert (WNT).
+      constexpr int BPOL = (BM == 32 || WNT) ? kCpolNT : 0;
 #pragma unroll
       for (int i = 0; i < B_INSTR; ++i) dma16<BPOL>(rB, sb + (wave * B_ROWS + i * RPIK) * PK, b_off[i], ka);
     }
@@ -1593,12 +1596,12 @@ int launch_mgemm(const void* A, const int32_t* gather, const void* W, const int6
   return HRM_MOE_OK;
 }
 
-template <typename TR, int KIND, int BM, int BN, int STAGES, int NW, int BK, int EPI = EPI_PLAIN>
+template <typename TR, int KIND, int BM, int BN, int STAGES, int NW, int BK, int EPI = EPI_PLAIN, bool WNT = false>
 int launch_mgemm_dma(const void* A, const int32_t* gather, const void* W, const int64_t* tpe, int64_t M, int N,
                      int K, int E, int64_t a_rows, void* C, void* workspace, void* stream, void* aux = nullptr) {
   (void)workspace;  // the DMA kernels plan their tiles themselves
   const int tiles_n = KIND == KIND_GATHER_SWIGLU ? (N + BN / 2 - 1) / (BN / 2) : (N + BN - 1) / BN;
-  auto kern = mgemm_dma_kernel<TR, KIND, BM, BN, STAGES, NW, BK, EPI>;
+  auto kern = mgemm_dma_kernel<TR, KIND, BM, BN, STAGES, NW, BK, EPI, WNT>;
   const size_t plan_bytes = sizeof(int) * 3 * (size_t)E;
   static int grid = 0, grid_e = -1;
   if (grid == 0 || grid_e != E) {
@@ -1722,6 +1725,12 @@ int dispatch_mgemm_t(const void* A, const int32_t* gather, const void* W, const 
     HRM_MG(128, 128, 4, 4, 32);
   }
   if (c.stages == 3) HRM_MG(128, 128, 3, 4, 64);
+  // experts averaging at most 128 rows (one M tile): weights read once, so
+  // loaded non-temporally (decode T = 256 108.6 -> 99.4 us, T = 512 113.5 ->
+  // 104.7 us; at L's 2048 rows per expert the same loads were much slower)
+  if (KIND != KIND_NN && M <= (int64_t)E * 128)
+    return launch_mgemm_dma<TR, KIND, 128, 128, 2, 4, 64, EPI_PLAIN, true>(A, gather, W, tpe, M, N, K, E, a_rows, C,
+                                                                          workspace, stream);
   HRM_MG(128, 128, 2, 4, 64);
 #undef HRM_MG
 }
