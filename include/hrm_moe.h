@@ -85,11 +85,12 @@ int hrm_moe_permute(const int64_t* topk_idx, int64_t num_tokens, int32_t num_exp
                     void* stream);
 
 /*
- * Router and dispatch in two launches: hrm_moe_router_topk, then
- * hrm_moe_permute on its topk_idx, with the same outputs.  The router kernel
- * also ranks each block's routed slots within their expert, and one
- * scan + scatter kernel finishes the dispatch.  Replaces models/layers.py:
- * 606-610 and :312-322 back to back.  sort_idx may be NULL.
+ * Router and dispatch in two launches (one up to 64 tokens): hrm_moe_router_topk,
+ * then hrm_moe_permute on its topk_idx, with the same outputs.  The router
+ * kernel also ranks each block's routed slots within their expert, and one
+ * scan + scatter kernel finishes the dispatch; with a single router block the
+ * router kernel finishes it itself.  Replaces models/layers.py:606-610 and
+ * :312-322 back to back.  sort_idx may be NULL.
  * Limits: E <= 128, k <= 8, T*k < 2^31.  Workspace:
  * hrm_moe_router_dispatch_workspace_size.
  */
