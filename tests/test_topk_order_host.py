@@ -83,3 +83,25 @@ def test_weight_sum_order_is_pairwise_for_eight(checker):
     w = np.take_along_axis(vals, got_idx, 1)
     pair = ((w[:, 0] + w[:, 1]) + (w[:, 2] + w[:, 3])) + ((w[:, 4] + w[:, 5]) + (w[:, 6] + w[:, 7]))
     assert np.array_equal(got_sum, pair.astype(np.float32))
+
+
+@pytest.mark.parametrize("loop_form", [0, 2])
+@pytest.mark.parametrize("k", [1, 2, 3, 4, 5, 6, 7, 8, 16, 32])
+def test_distinct_and_tied_rows_mixed(checker, k, loop_form):
+    """Rows whose selected keys are all distinct (torch's order is then plain
+    descending order) mixed with rows that have ties among them, against the
+    oracle and against the loop form's weight sums."""
+    if loop_form == 2 and k not in (2, 4, 8, 16, 32):
+        pytest.skip("the compile-time form exists for k == SLOTS only")
+    rng = np.random.default_rng(500 + k)
+    vals = rng.random((800, 64)).astype(np.float32)
+    tied = rng.random(800) < 0.3
+    vals[tied] = (rng.integers(0, 5, size=(int(tied.sum()), 64)).astype(np.float32) * 0.125 + 0.0625)
+    got, got_sum = run_checker(checker, vals, k, loop_form)
+    _, want = mo.topk_rocm(vals, k)
+    assert np.array_equal(got, want)
+    _, mem_sum = run_checker(checker, vals, k, 1)
+    assert np.array_equal(got_sum, mem_sum)
+    # distinct rows: torch's order is the descending (value, then index) order
+    order = np.lexsort((np.broadcast_to(np.arange(64), vals.shape), -vals), axis=-1)[:, :k]
+    assert np.array_equal(got[~tied], order[~tied])
