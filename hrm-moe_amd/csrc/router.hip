@@ -24,6 +24,8 @@
 //    experts hold exp(-inf) = 0, which leaves every partial sum unchanged.
 //  * top-k: selection in (value desc, index asc) order, then torch's output
 //    order and weight-sum order from topk_order.h.
+#include <stdlib.h>
+
 #include "common.h"
 #include "topk_order.h"
 
@@ -443,6 +445,177 @@ __global__ __launch_bounds__(kBwdTokPerBlock * 64) void router_bwd_kernel(
   }
 }
 
+// Decode sizes (T <= 16 tokens, E <= 64, k <= 8): router and the whole
+// dispatch in one block, one wave per token, lane e holding expert e.  A
+// wave of the quad kernel runs the same serial chain (k arg-max rounds over
+// 16 experts per lane, then the ordering network) whether it holds 16 rows or
+// one; here each step is a handful of instructions.  Same arithmetic as
+// router_topk_kernel, so the outputs are the same bits:
+//  * softmax: the xor butterfly over lanes at distances 32 ... 1 is the
+//    pairwise tree S_e <- S_e + S_(e^o) that the quad kernel evaluates
+//    (cross-lane levels, then in-lane levels); fp32 addition commutes, so
+//    both lanes of a pair hold the same bits.  Padding lanes hold 0.
+//  * selection: each lane counts the (key, ~index) pairs above its own, i.e.
+//    its rank in (key desc, index asc) order; ranks 0..k-1 are the k arg-max
+//    rounds' winners in round order.  A round with no selectable key left
+//    (key 0) yields index INT_MAX, as in the arg-max rounds.
+//  * torch's output order equals that order unless two of the k keys are
+//    equal (the network sorts distinct keys descending), so the ordering
+//    network runs only then: a wave-uniform branch, one token per wave.
+//  * weight sum in torch's order, IEEE division.
+//  * dispatch: stable counting sort of the T*k slots by bucket (expert, or E
+//    for an id outside [0, E)) with the rank step's LDS bitmasks.
+constexpr int kWaveRouterMaxTokens = 16;
+
+template <int SLOTS, bool KFIX>
+__global__ __launch_bounds__(64 * kWaveRouterMaxTokens) void router_dispatch_wave_kernel(
+    const void* __restrict__ logits, int ldt, int T, int E, int k_rt, int norm, float* __restrict__ probs,
+    int64_t* __restrict__ idx_out, void* __restrict__ w_out, int wdt, DispatchOut dout) {
+  static_assert(SLOTS <= 8, "k <= 8");
+  constexpr int KC = KFIX ? SLOTS : 0;
+  constexpr int kMaxWords = (kWaveRouterMaxTokens * 8 + 31) / 32;
+  const int k = KFIX ? SLOTS : k_rt;
+  const int lane = threadIdx.x & 63;
+  const int t = threadIdx.x >> 6;  // this wave's token; the block has T waves
+  __shared__ uint64_t s_ck[kWaveRouterMaxTokens][64];
+  __shared__ uint32_t s_sk[kWaveRouterMaxTokens][SLOTS];
+  __shared__ int32_t s_si[kWaveRouterMaxTokens][SLOTS];
+  __shared__ uint32_t s_mask[65 * kMaxWords];
+  __shared__ uint32_t s_pref[65 * kMaxWords];
+  __shared__ int32_t s_off[65];
+
+  const bool ok = lane < E;
+  const float x = ok ? load_logit(logits, ldt, (int64_t)t * E + lane) : -INFINITY;
+  float mx = x;
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
+  const float s = expf(x - mx);
+  float total = s;
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) total = total + __shfl_xor(total, o, 64);
+  const float p = s / total;
+  if (ok && probs != nullptr) probs[(int64_t)t * E + lane] = p;
+  const uint32_t key = ok ? (__float_as_uint(p) + 1u) : 0u;  // 0 marks "not selectable"
+
+  // rank among the wave's 64 unique (key, 63 - lane) pairs
+  const uint64_t ck = ((uint64_t)key << 32) | (uint32_t)(63 - lane);
+  s_ck[t][lane] = ck;
+  __syncthreads();
+  int rank = 0;
+#pragma unroll
+  for (int j = 0; j < 64; ++j) rank += s_ck[t][j] > ck ? 1 : 0;
+  if (rank < k) {
+    s_sk[t][rank] = key;
+    s_si[t][rank] = key != 0u ? lane : 0x7fffffff;
+  }
+  __syncthreads();
+  uint32_t sk[SLOTS];
+  int si[SLOTS];
+#pragma unroll
+  for (int r = 0; r < SLOTS; ++r) {
+    sk[r] = r < k ? s_sk[t][r] : 0u;
+    si[r] = r < k ? s_si[t][r] : 0;
+  }
+  bool tie = false;
+#pragma unroll
+  for (int r = 0; r + 1 < SLOTS; ++r) tie = tie || (r + 1 < k && sk[r] == sk[r + 1]);
+  uint32_t gk[SLOTS];
+  int gi[SLOTS];
+  if (__builtin_amdgcn_readfirstlane((int)tie)) {
+    torch_topk_order<SLOTS, KC>(sk, si, k, gk, gi);
+  } else {
+#pragma unroll
+    for (int r = 0; r < SLOTS; ++r) {
+      gk[r] = sk[r];
+      gi[r] = si[r];
+    }
+  }
+  float w[SLOTS];
+#pragma unroll
+  for (int j = 0; j < SLOTS; ++j) w[j] = __uint_as_float(gk[j] - 1u);
+  if (norm) {
+    float sum = torch_row_sum<SLOTS, KC>(w, k);
+    sum = (sum != sum) ? sum : fmaxf(sum, 1e-12f);
+#pragma unroll
+    for (int j = 0; j < SLOTS; ++j) w[j] = w[j] / sum;
+  }
+  int my_i = 0;
+  float my_w = 0.0f;
+#pragma unroll
+  for (int j = 0; j < SLOTS; ++j) {
+    my_i = lane == j ? gi[j] : my_i;
+    my_w = lane == j ? w[j] : my_w;
+  }
+  const bool slot = lane < k;
+  const int ls = t * k + lane;  // flat slot index
+  if (slot) {
+    idx_out[ls] = (int64_t)my_i;
+    store_weight(w_out, wdt, ls, my_w);
+  }
+
+  // dispatch of the block's T*k slots
+  const int nbk = E + 1;
+  const int words = (T * k + 31) / 32;
+  for (int i = threadIdx.x; i < nbk * words; i += blockDim.x) s_mask[i] = 0u;
+  __syncthreads();
+  const int b = (my_i >= 0 && my_i < E) ? my_i : E;
+  if (slot) atomicOr(&s_mask[b * words + (ls >> 5)], 1u << (ls & 31));
+  __syncthreads();
+  for (int c = threadIdx.x; c < nbk; c += blockDim.x) {
+    uint32_t run = 0;
+    for (int w2 = 0; w2 < words; ++w2) {
+      s_pref[c * words + w2] = run;
+      run += __popc(s_mask[c * words + w2]);
+    }
+    s_off[c] = (int32_t)run;
+  }
+  __syncthreads();
+  if (threadIdx.x < 64) {  // bucket totals -> exclusive offsets
+    int32_t carry = 0;
+    for (int c0 = 0; c0 < nbk; c0 += 64) {
+      const int c = c0 + lane;
+      const int32_t v = c < nbk ? s_off[c] : 0;
+      int32_t incl = v;
+#pragma unroll
+      for (int o = 1; o < 64; o <<= 1) {
+        const int32_t u = __shfl_up(incl, o, 64);
+        if (lane >= o) incl += u;
+      }
+      if (c < nbk) {
+        if (c < E) dout.tokens_per_expert[c] = (int64_t)v;
+        s_off[c] = carry + incl - v;
+        dout.expert_offsets[c] = carry + incl - v;
+      }
+      carry += __shfl(incl, 63, 64);
+    }
+  }
+  __syncthreads();
+  if (slot) {
+    const uint32_t below = s_mask[b * words + (ls >> 5)] & ((1u << (ls & 31)) - 1u);
+    const int32_t dst = s_off[b] + (int32_t)(s_pref[b * words + (ls >> 5)] + __popc(below));
+    dout.sorted_token_idx[dst] = t;
+    if (dout.sort_idx) dout.sort_idx[dst] = ls;
+    dout.slot_to_row[ls] = dst;
+  }
+}
+
+// T <= 16 tokens, E <= 64, k <= 8: one block of T waves.
+int launch_router_dispatch_wave(const void* logits, int ldt, int64_t T, int E, int k, int norm, float* probs,
+                                int64_t* idx, void* w, int wdt, const DispatchOut& dout, void* stream) {
+  const dim3 grid(1), block((unsigned)(64 * T));
+#define HRM_RW(SL, KF)                                                                                               \
+  HRM_LAUNCH((router_dispatch_wave_kernel<SL, KF>), grid, block, 0, stream, logits, ldt, (int)T, E, k, norm, probs, \
+             idx, w, wdt, dout)
+  if (k == 2) HRM_RW(2, true);
+  else if (k == 4) HRM_RW(4, true);
+  else if (k == 8) HRM_RW(8, true);
+  else if (k <= 2) HRM_RW(2, false);
+  else if (k <= 4) HRM_RW(4, false);
+  else HRM_RW(8, false);
+#undef HRM_RW
+  return HRM_MOE_OK;
+}
+
 }  // namespace
 }  // namespace hrm
 
@@ -527,6 +700,12 @@ extern "C" int hrm_moe_router_topk_dispatch(const void* logits, int logits_dtype
     // up to 64 tokens: one router block finishes the dispatch itself (no second launch)
     const bool solo = nb == 1;
     const hrm::DispatchOut dout{tokens_per_expert, expert_offsets, sorted_token_idx, sort_idx, slot_to_row};
+    // up to 16 tokens and 64 experts: one wave per token (HRM_MOE_WAVE_ROUTER=0
+    // selects the quad kernel instead; read per call so tests can compare both)
+    const char* wr = getenv("HRM_MOE_WAVE_ROUTER");
+    if (num_tokens <= hrm::kWaveRouterMaxTokens && E <= 64 && !(wr && wr[0] == '0'))
+      return hrm::launch_router_dispatch_wave(logits, logits_dtype, num_tokens, E, k, norm_topk_prob, probs, topk_idx,
+                                              topk_weight, weight_dtype, dout, stream);
     int st;
     if (E <= 8)
       st = hrm::launch_router_rank<8>(logits, logits_dtype, num_tokens, E, k, norm_topk_prob, probs, topk_idx,

@@ -89,7 +89,10 @@ int hrm_moe_permute(const int64_t* topk_idx, int64_t num_tokens, int32_t num_exp
  * then hrm_moe_permute on its topk_idx, with the same outputs.  The router
  * kernel also ranks each block's routed slots within their expert, and one
  * scan + scatter kernel finishes the dispatch; with a single router block the
- * router kernel finishes it itself.  Replaces models/layers.py:606-610 and
+ * router kernel finishes it itself.  Up to 16 tokens with E <= 64, one block
+ * with a wave per token (lane e holds expert e) does all of it; environment
+ * HRM_MOE_WAVE_ROUTER=0 keeps the quad-layout kernel there.  Outputs are the
+ * same bits either way.  Replaces models/layers.py:606-610 and
  * :312-322 back to back.  sort_idx may be NULL.
  * Limits: E <= 128, k <= 8, T*k < 2^31.  Workspace:
  * hrm_moe_router_dispatch_workspace_size.

@@ -99,3 +99,39 @@ def test_router_dispatch_zero_tokens(cuda):
     _, w, idx, d = ops.router_topk_dispatch(lg, 8, True, torch.bfloat16, want_probs=False)
     assert idx.shape == (0, 8) and int(d.tokens_per_expert.abs().sum()) == 0
     assert int(d.expert_offsets.abs().sum()) == 0
+
+
+@pytest.mark.parametrize("wave", ["1", "0"])
+@pytest.mark.parametrize("t,e,k,ldt,wdt,norm,levels", [
+    (1, 64, 8, torch.bfloat16, torch.bfloat16, True, 0), (8, 64, 8, torch.bfloat16, torch.bfloat16, True, 0),
+    (16, 64, 8, torch.bfloat16, torch.bfloat16, True, 0), (5, 48, 6, torch.bfloat16, torch.bfloat16, True, 0),
+    (3, 8, 2, torch.float32, torch.float32, True, 0), (16, 16, 1, torch.float16, torch.float16, False, 0),
+    (7, 64, 4, torch.float32, torch.bfloat16, False, 0), (11, 33, 3, torch.bfloat16, torch.float32, True, 0),
+    # exact ties inside and at the edge of the top k
+    (16, 64, 8, torch.bfloat16, torch.bfloat16, True, 3), (16, 64, 8, torch.bfloat16, torch.bfloat16, True, 6),
+    (9, 64, 5, torch.bfloat16, torch.bfloat16, True, 2), (16, 8, 8, torch.bfloat16, torch.bfloat16, True, 2),
+    (12, 64, 2, torch.bfloat16, torch.bfloat16, False, 4), (1, 64, 8, torch.bfloat16, torch.bfloat16, True, 1)])
+def test_router_dispatch_decode_sizes(cuda, monkeypatch, wave, t, e, k, ldt, wdt, norm, levels):
+    """Up to 16 tokens: the one-wave-per-token kernel (and the quad kernel it replaces) give the bits of
+    router_topk followed by permute, ties included; the indices and weights also equal torch's on the device."""
+    monkeypatch.setenv("HRM_MOE_WAVE_ROUTER", wave)
+    rng = np.random.default_rng(1000 * t + 10 * e + k + levels)
+    if levels:
+        z = rng.integers(0, levels, size=(t, e)).astype(np.float32) * 0.25
+    else:
+        z = rng.standard_normal((t, e)).astype(np.float32)
+    lg = torch.from_numpy(z).to(ldt).to(cuda)
+    probs, w, idx, d = ops.router_topk_dispatch(lg, k, norm, wdt, want_probs=True, want_sort_idx=True)
+    probs2, w2, idx2 = ops.router_topk(lg, k, norm, wdt)
+    d2 = ops.permute(idx2, e, want_sort_idx=True)
+    assert torch.equal(idx, idx2) and torch.equal(w.view(-1).float(), w2.view(-1).float())
+    assert torch.equal(probs.view(torch.int32), probs2.view(torch.int32))
+    for name in ("tokens_per_expert", "expert_offsets", "sorted_token_idx", "slot_to_row", "sort_idx"):
+        assert torch.equal(getattr(d, name), getattr(d2, name)), name
+    rp = torch.softmax(lg, dim=-1, dtype=torch.float32)
+    rw, ri = torch.topk(rp, k, dim=-1)
+    if norm:
+        rw = rw / rw.sum(dim=-1, keepdim=True).clamp_min(1e-12)
+    assert torch.equal(idx, ri), "top-k indices differ from torch.topk on the device"
+    assert torch.equal(w.float(), rw.to(wdt).float()), "weights differ from torch on the device"
+    assert torch.equal(probs.view(torch.int32), rp.view(torch.int32))
