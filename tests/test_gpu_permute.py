@@ -110,9 +110,13 @@ def test_router_dispatch_zero_tokens(cuda):
     # exact ties inside and at the edge of the top k
     (16, 64, 8, torch.bfloat16, torch.bfloat16, True, 3), (16, 64, 8, torch.bfloat16, torch.bfloat16, True, 6),
     (9, 64, 5, torch.bfloat16, torch.bfloat16, True, 2), (16, 8, 8, torch.bfloat16, torch.bfloat16, True, 2),
-    (12, 64, 2, torch.bfloat16, torch.bfloat16, False, 4), (1, 64, 8, torch.bfloat16, torch.bfloat16, True, 1)])
+    (12, 64, 2, torch.bfloat16, torch.bfloat16, False, 4), (1, 64, 8, torch.bfloat16, torch.bfloat16, True, 1),
+    # 17..64 tokens: the single-block quad kernel
+    (17, 64, 8, torch.bfloat16, torch.bfloat16, True, 0), (64, 64, 8, torch.bfloat16, torch.bfloat16, True, 0),
+    (50, 40, 5, torch.float32, torch.float16, True, 0), (64, 64, 8, torch.bfloat16, torch.bfloat16, True, 3),
+    (33, 8, 2, torch.bfloat16, torch.bfloat16, False, 2), (63, 64, 7, torch.bfloat16, torch.float32, True, 5)])
 def test_router_dispatch_decode_sizes(cuda, monkeypatch, wave, t, e, k, ldt, wdt, norm, levels):
-    """Up to 16 tokens: the one-wave-per-token kernel (and the quad kernel it replaces) give the bits of
+    """Up to 64 tokens (the wave-per-token kernel up to 16, the quad kernel in both settings above) give the bits of
     router_topk followed by permute, ties included; the indices and weights also equal torch's on the device."""
     monkeypatch.setenv("HRM_MOE_WAVE_ROUTER", wave)
     rng = np.random.default_rng(1000 * t + 10 * e + k + levels)
