@@ -912,37 +912,108 @@ __global__ __launch_bounds__(NW * 64, NW == 4 ? 2 : 1) void mgemm_dma_kernel(con
 #pragma unroll
         for (int v = 0; v < 16; ++v) acc[b][a][v] = 0.0f;
 
-    for (int kt = 0; kt < nk; ++kt) {
-      const int gs = g0 + kt;
-      wait_stages<PER, STAGES - 2>(min(STAGES - 2, issued - gs - 1));
-      barrier_lds();
-      if (issued == gs + STAGES - 1) issue_next();
-      const char* la = smem + (gs % STAGES) * STAGE_BYTES;
-      const char* lb = la + A_BYTES;
-      u32x4 fw[2][NB], fa[2][MBH];
-      auto load_frags = [&](int s, u32x4 (&w)[NB], u32x4 (&x)[MBH]) __attribute__((always_inline)) {
+    // K loop over MBV of the wave's MBH 32-row blocks: blocks wholly past the
+    // tile's last row (an expert's ragged last M tile) get no fragment reads
+    // and no MFMAs, which leaves the SIMD's matrix pipe to the other wave on
+    // it (down GEMM: L 184 -> 181 us, XL128 471 -> 461 us).  Their accumulators stay zero; the epilogue's stores past the last
+    // row fall outside the output's buffer range.  Every wave still waits,
+    // passes each barrier and issues its share of the DMA.
+    auto kloop = [&](auto mbv_tag) __attribute__((always_inline)) {
+      constexpr int MBV = decltype(mbv_tag)::value;
+      for (int kt = 0; kt < nk; ++kt) {
+        const int gs = g0 + kt;
+        wait_stages<PER, STAGES - 2>(min(STAGES - 2, issued - gs - 1));
+        barrier_lds();
+        if (issued == gs + STAGES - 1) issue_next();
+        if constexpr (MBV > 0) {
+          const char* la = smem + (gs % STAGES) * STAGE_BYTES;
+          const char* lb = la + A_BYTES;
+          u32x4 fw[2][NB], fa[2][MBV];
+          auto load_frags = [&](int s, u32x4 (&w)[NB], u32x4 (&x)[MBV]) __attribute__((always_inline)) {
 #pragma unroll
-        for (int b = 0; b < NB; ++b) {
-          int r0;
-          if constexpr (KIND == KIND_GATHER_SWIGLU)  // gate blocks, then the matching up blocks
-            r0 = (b < NB / 2 ? 0 : BN / 2) + col_blk + (b % (NB / 2)) * 32;
-          else
-            r0 = wn * (BN / WGN) + b * 32;
-          if constexpr (KIND == KIND_NN) w[b] = tr_operand<BN>(lb, r0, s, lane);
-          else w[b] = lds_read16(lb, kcp_off<PK>(r0 + (lane & 31), s * 2 + (lane >> 5)));
+            for (int b = 0; b < NB; ++b) {
+              int r0;
+              if constexpr (KIND == KIND_GATHER_SWIGLU)  // gate blocks, then the matching up blocks
+                r0 = (b < NB / 2 ? 0 : BN / 2) + col_blk + (b % (NB / 2)) * 32;
+              else
+                r0 = wn * (BN / WGN) + b * 32;
+              if constexpr (KIND == KIND_NN) w[b] = tr_operand<BN>(lb, r0, s, lane);
+              else w[b] = lds_read16(lb, kcp_off<PK>(r0 + (lane & 31), s * 2 + (lane >> 5)));
+            }
+#pragma unroll
+            for (int a = 0; a < MBV; ++a)
+              x[a] = lds_read16(la, kcp_off<PK>(row_base + a * 32 + (lane & 31), s * 2 + (lane >> 5)));
+          };
+          load_frags(0, fw[0], fa[0]);
+#pragma unroll
+          for (int s = 0; s < BK / 16; ++s) {
+            if (s + 1 < BK / 16) load_frags(s + 1, fw[(s + 1) & 1], fa[(s + 1) & 1]);
+#pragma unroll
+            for (int b = 0; b < NB; ++b)
+#pragma unroll
+              for (int a = 0; a < MBV; ++a) acc[b][a] = TR::mfma32(fw[s & 1][b], fa[s & 1][a], acc[b][a]);
+          }
         }
+      }
+    };
+    // Down projection and dgrad only.  The gather + gate/up kernel keeps the
+    // plain loop: its code built through kloop measured 1-2% slower (L
+    // gate_up +3 us, XL128 +14 us, paired launches), even with every row
+    // block valid.
+    if constexpr (H || KIND == KIND_GATHER_SWIGLU) {
+      for (int kt = 0; kt < nk; ++kt) {
+        const int gs = g0 + kt;
+        wait_stages<PER, STAGES - 2>(min(STAGES - 2, issued - gs - 1));
+        barrier_lds();
+        if (issued == gs + STAGES - 1) issue_next();
+        const char* la = smem + (gs % STAGES) * STAGE_BYTES;
+        const char* lb = la + A_BYTES;
+        u32x4 fw[2][NB], fa[2][MBH];
+        auto load_frags = [&](int s, u32x4 (&w)[NB], u32x4 (&x)[MBH]) __attribute__((always_inline)) {
 #pragma unroll
-        for (int a = 0; a < MBH; ++a)
-          x[a] = lds_read16(la, kcp_off<PK>(row_base + a * 32 + (lane & 31), s * 2 + (lane >> 5)));
-      };
-      load_frags(0, fw[0], fa[0]);
+          for (int b = 0; b < NB; ++b) {
+            int r0;
+            if constexpr (KIND == KIND_GATHER_SWIGLU)  // gate blocks, then the matching up blocks
+              r0 = (b < NB / 2 ? 0 : BN / 2) + col_blk + (b % (NB / 2)) * 32;
+            else
+              r0 = wn * (BN / WGN) + b * 32;
+            if constexpr (KIND == KIND_NN) w[b] = tr_operand<BN>(lb, r0, s, lane);
+            else w[b] = lds_read16(lb, kcp_off<PK>(r0 + (lane & 31), s * 2 + (lane >> 5)));
+          }
 #pragma unroll
-      for (int s = 0; s < BK / 16; ++s) {
-        if (s + 1 < BK / 16) load_frags(s + 1, fw[(s + 1) & 1], fa[(s + 1) & 1]);
+          for (int a = 0; a < MBH; ++a)
+            x[a] = lds_read16(la, kcp_off<PK>(row_base + a * 32 + (lane & 31), s * 2 + (lane >> 5)));
+        };
+        load_frags(0, fw[0], fa[0]);
 #pragma unroll
-        for (int b = 0; b < NB; ++b)
+        for (int s = 0; s < BK / 16; ++s) {
+          if (s + 1 < BK / 16) load_frags(s + 1, fw[(s + 1) & 1], fa[(s + 1) & 1]);
 #pragma unroll
-          for (int a = 0; a < MBH; ++a) acc[b][a] = TR::mfma32(fw[s & 1][b], fa[s & 1][a], acc[b][a]);
+          for (int b = 0; b < NB; ++b)
+#pragma unroll
+            for (int a = 0; a < MBH; ++a) acc[b][a] = TR::mfma32(fw[s & 1][b], fa[s & 1][a], acc[b][a]);
+        }
+      }
+    } else {
+      // this wave's 32-row blocks that hold a row of the tile (wave-uniform)
+      const int vrows = __builtin_amdgcn_readfirstlane(comp_re - comp_rs) - row_base;
+      const int nvb = vrows <= 0 ? 0 : min((vrows + 31) / 32, MBH);
+      using I0 = std::integral_constant<int, 0>;
+      using I1 = std::integral_constant<int, 1>;
+      using I2 = std::integral_constant<int, 2>;
+      using I3 = std::integral_constant<int, 3>;
+      if (nvb >= MBH) {
+        kloop(std::integral_constant<int, MBH>{});
+      } else if constexpr (MBH == 4) {
+        if (nvb == 3) kloop(I3{});
+        else if (nvb == 2) kloop(I2{});
+        else if (nvb == 1) kloop(I1{});
+        else kloop(I0{});
+      } else if constexpr (MBH == 2) {
+        if (nvb == 1) kloop(I1{});
+        else kloop(I0{});
+      } else {
+        kloop(I0{});
       }
     }
 
