@@ -175,3 +175,29 @@ def test_grouped_gemm_deterministic(cuda):
     d1 = ops.grouped_gemm_tn(y1, a, tpe)
     d2 = ops.grouped_gemm_tn(y2, a, tpe)
     assert torch.equal(y1, y2) and torch.equal(d1, d2)
+
+
+# Row counts on both sides of every 32-row block edge of 128- and 256-row
+# tiles, plus empty experts: the last M tile of an expert runs only the row
+# blocks that hold rows (down and dgrad kernels).
+EDGE_TPE = np.array([1, 31, 32, 33, 0, 63, 64, 65, 95, 96, 97, 127, 128, 129, 0, 159, 191, 223, 255, 256, 257,
+                     288, 289, 383, 385, 511, 513], np.int64)
+
+
+@pytest.mark.parametrize("cfg", ["", "128x128x2x4x64", "256x256x2x8x64"])
+def test_grouped_gemm_row_block_edges(cuda, monkeypatch, cfg):
+    monkeypatch.setenv("HRM_MOE_GEMM_CFG", cfg)
+    e, m = EDGE_TPE.size, int(EDGE_TPE.sum())
+    n, k = 512, 448
+    tpe = torch.from_numpy(EDGE_TPE).to(cuda)
+    a = torch.from_numpy(synth.normal(11, (m, k))).to(torch.bfloat16)
+    w = torch.from_numpy(synth.normal(12, (e, n, k), std=0.05)).to(torch.bfloat16)
+    got = ops.grouped_gemm_nt(a.to(cuda), w.to(cuda), tpe)
+    close(got, mo.grouped_linear(a, w, EDGE_TPE), f"nt edges {cfg}")
+    g = torch.from_numpy(synth.normal(13, (m, n))).to(torch.bfloat16)
+    dg = ops.grouped_gemm_nn(g.to(cuda), w.to(cuda), tpe)
+    close(dg, mo.grouped_linear_dgrad(g, w, EDGE_TPE), f"nn edges {cfg}")
+    # the tile shapes accumulate K in the same order: identical bits
+    monkeypatch.setenv("HRM_MOE_GEMM_CFG", "128x128x2x4x64")
+    assert torch.equal(got, ops.grouped_gemm_nt(a.to(cuda), w.to(cuda), tpe))
+    assert torch.equal(dg, ops.grouped_gemm_nn(g.to(cuda), w.to(cuda), tpe))
