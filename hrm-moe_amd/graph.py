@@ -23,9 +23,12 @@ from .layers import SparseMoESwiGLU
 class GraphedMoEForward:
     """Replays ``layer(x)`` (no autograd) from a HIP graph captured for ``example``'s shape and dtype.
 
-    The call copies ``x`` into the captured input buffer, replays the graph
-    and returns the captured output buffer: the next call overwrites it, so
-    keep a copy if the result must outlive that.  The graph holds the
+    The call copies ``x`` into the captured input buffer ``static_in``,
+    replays the graph and returns the captured output buffer: the next call
+    overwrites it, so keep a copy if the result must outlive that.  A caller
+    that writes the step's tokens into ``static_in`` itself (e.g. as the
+    output buffer of the op before) passes ``static_in`` and skips the copy,
+    one kernel launch per step.  The graph holds the
     addresses of the layer's parameters; in-place updates of them are seen by
     later replays, replaced parameter tensors are not (capture again).
     """
@@ -50,6 +53,7 @@ class GraphedMoEForward:
         if x.shape != self.static_in.shape or x.dtype != self.static_in.dtype or x.device != self.static_in.device:
             raise ValueError(f"graph captured for {tuple(self.static_in.shape)} {self.static_in.dtype} on "
                              f"{self.static_in.device}, got {tuple(x.shape)} {x.dtype} on {x.device}")
-        self.static_in.copy_(x)
+        if x.data_ptr() != self.static_in.data_ptr():
+            self.static_in.copy_(x)
         self.graph.replay()
         return self.static_out

@@ -40,6 +40,14 @@ def test_graph_replay_matches_eager(cuda, t):
         noise = noise @ noise.T / 512.0  # eager work between replays
         torch.cuda.synchronize()
         assert torch.equal(out, ref), f"replay {rep} differs from the eager forward"
+    # tokens written into the captured input buffer by the caller: no copy, same results
+    for rep in range(4):
+        x, ref = (x2, e2) if rep % 2 == 0 else (x1, e1)
+        g.static_in.copy_(x)
+        noise = noise @ noise.T / 512.0
+        out = g(g.static_in).clone()
+        torch.cuda.synchronize()
+        assert torch.equal(out, ref), f"in-place replay {rep} differs from the eager forward"
 
 
 def test_graph_rejects_other_shapes(cuda):
