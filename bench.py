@@ -9,11 +9,18 @@ Infinity Cache cannot keep one layer's 220 MB of expert weights.
 
 Printed (one JSON line on stdout): active TFLOP/s of the layer (6*R*H*I per
 step, R = T*k) and ms per layer over the timed steps; per-op times from a
-second pass of the same steps with HIP events around every op (events stall
-the stream for a few microseconds each, so they stay out of the headline
-pass); the roofline of the dominant kernel (fused gate_up + SwiGLU GEMM, from
-those events on its stream) and the reference's eager CPU path timed on the
-host's cores over a bounded sample.
+separate pass of the same workload with HIP events around every op (events
+stall the stream for a few microseconds each, so they stay out of the
+headline pass); the roofline of the dominant kernel (fused gate_up + SwiGLU
+GEMM, from those events on its stream, with the HBM traffic of a committed
+counter summary when it describes the kernel that ran) and the reference's
+eager CPU path timed on the host's cores.
+
+Pass order: the per-op pass runs first, over at least 60 layer forwards.  The
+GPU's clocks take a few tens of milliseconds of load to settle after idling
+(the first 20 forwards after 5 warmup steps measured 0.67 ms per layer, later
+windows 0.59-0.60 ms), so the headline pass that follows, W warmup steps and
+then exactly K timed steps, is measured at the settled clock.
 
 Usage: python bench.py [--steps K] [--warmup W] [--gpus 1]
                        [--workload l64x8|xl_skew|xl128|decode_t{1,8,64,256}|xl128_train|l64x8_train|xl_skew_train]
@@ -122,7 +129,7 @@ def time_layers(layers, xs, steps, warmup, timer=None):
 
     Each timed event costs the stream a few microseconds of idle time, so the
     headline layer time is taken with timer=None and the per-op times in a
-    second pass over the same workload.
+    separate pass over the same workload.
     """
     with torch.no_grad():
         for s in range(warmup):
@@ -155,45 +162,95 @@ def calibrate_copy(mb, reps=5):
     print(json.dumps({"calibrate_copy_bytes_read": n, "calibrate_copy_bytes_written": n, "reps": reps}), flush=True)
 
 
-def read_traffic(name):
-    """HBM bytes per launch from a committed rocprofv3 --pmc summary, if one exists."""
+def read_traffic(name, kernel):
+    """HBM traffic per launch of ``kernel`` from a committed rocprofv3 --pmc summary under profiles/.
+
+    The summary names the kernel instantiation it measured (``kernel:`` line);
+    when that is not ``kernel`` (the instantiation this run launched), the
+    figures describe other code and None is returned.  Bytes are FETCH_SIZE and
+    WRITE_SIZE per dispatch, scaled by what the counters read for a plain copy
+    of known size; FETCH_SIZE counts L2 misses, Infinity Cache hits included.
+    """
     path = os.path.join(ROOT, "profiles", name)
-    if not os.path.exists(path):
+    if not os.path.exists(path) or not kernel:
         return None
+    fields = {}
     for line in open(path):
-        if line.startswith("hbm_bytes_per_launch:"):
-            return int(float(line.split(":", 1)[1].strip()))
-    return None
+        key, sep, val = line.partition(":")
+        if sep and key in ("kernel", "fetch_bytes_per_launch", "write_bytes_per_launch",
+                           "algorithmic_bytes_per_launch", "expert_partitioned_min_bytes_per_launch"):
+            fields[key] = val.strip()
+    if fields.get("kernel") != kernel:
+        log(f"traffic summary {name} describes {fields.get('kernel')!r}, this run launched {kernel!r}: not used")
+        return None
+    out = {"kernel": kernel, "source": f"profiles/{name}"}
+    for key in ("fetch_bytes_per_launch", "write_bytes_per_launch", "algorithmic_bytes_per_launch",
+                "expert_partitioned_min_bytes_per_launch"):
+        if key in fields:
+            out[key] = int(float(fields[key]))
+    return out
 
 
-def cpu_baseline(t, h, e, i, k, sample_tokens=2048, runs=5):
-    """The reference's eager CPU path (oracle.moe_forward_eager) on a bounded sample of the workload."""
-    from oracle import moe_oracle, synth
+def _cpu_layer_inputs(t, h, e, i, bias_std, dtype, seed=1234):
+    """Synthetic inputs of one layer on the CPU, built like make_layer's (N(0,1) tokens, N(0, 0.02) weights)."""
+    g = torch.Generator().manual_seed(seed)
+    x = torch.randn(t, h, generator=g)
+    wg = torch.randn(e, h, generator=g) * 0.02
+    wgu = torch.randn(e, 2 * i, h, generator=g) * 0.02
+    wdn = torch.randn(e, h, i, generator=g) * 0.02
+    if bias_std > 0:
+        b = torch.randn(e, generator=g, dtype=torch.float64) * bias_std
+        wg64 = wg.double()
+        x = (x.double() + (wg64.T @ torch.linalg.solve(wg64 @ wg64.T, b))[None, :]).float()
+    return [a.to(dtype) for a in (x, wg, wgu, wdn)]
 
-    x, wg, wgu, wdn = synth.moe_inputs(1, sample_tokens, h, e, i)
-    args = [torch.from_numpy(a).to(torch.bfloat16) for a in (x, wg, wgu, wdn)]
+
+def _time_cpu_layer(t, h, e, i, k, bias_std, dtype, runs):
+    """Median seconds of the reference's eager CPU layer forward (oracle.moe_forward_eager) over ``runs``."""
+    from oracle import moe_oracle
+
+    args = _cpu_layer_inputs(t, h, e, i, bias_std, dtype)
     moe_oracle.moe_forward_eager(*args, k)
     ts = []
     for _ in range(runs):
         t0 = time.perf_counter()
         moe_oracle.moe_forward_eager(*args, k)
         ts.append(time.perf_counter() - t0)
-    sec = statistics.median(ts)
-    flops = 6.0 * sample_tokens * k * h * i
+    return statistics.median(ts)
+
+
+def cpu_baseline(t, h, e, i, k, bias_std=0.0, runs=5, legs=()):
+    """The reference's eager CPU path on the host cores: the bench's layer at full size in bf16.
+
+    ``legs``: more (name, T, H, E, I, k, bias, dtype) layers timed the same way,
+    reported beside the headline leg (the L and XL-skew shapes in bf16 and fp32).
+    """
     try:
         affinity = len(os.sched_getaffinity(0))
     except AttributeError:
         affinity = os.cpu_count()
-    return {
+    sec = _time_cpu_layer(t, h, e, i, k, bias_std, torch.bfloat16, runs)
+    flops = 6.0 * t * k * h * i
+    out = {
         "value": round(flops / sec / 1e12, 5),
         "unit": "TFLOP/s",
         "cores": torch.get_num_threads(),
         "kind": "port",
-        "sample": (f"{sample_tokens} of {t} tokens of the same layer shape, bf16, reference eager CPU path "
-                   f"(per-expert F.linear), median of {runs} runs after 1 warmup: {sec * 1e3:.1f} ms; "
-                   f"os.cpu_count()={os.cpu_count()}, affinity={affinity}"),
-        "ms_per_layer_extrapolated": round(sec * 1e3 * t / sample_tokens, 4),
+        "sample": (f"the whole layer ({t} tokens, bf16), reference eager CPU path (router, stable sort, per-expert "
+                   f"F.linear, index_add_), median of {runs} runs after 1 warmup: {sec * 1e3:.1f} ms; "
+                   f"torch threads {torch.get_num_threads()}, os.cpu_count()={os.cpu_count()}, affinity={affinity}"),
+        "ms_per_layer": round(sec * 1e3, 3),
     }
+    extra = []
+    for name, lt, lh, le, li, lk, lb, ldt in legs:
+        sec = _time_cpu_layer(lt, lh, le, li, lk, lb, ldt, runs)
+        extra.append({"leg": name, "dtype": str(ldt).replace("torch.", ""), "tokens": lt,
+                      "ms_per_layer": round(sec * 1e3, 3),
+                      "tflops": round(6.0 * lt * lk * lh * li / sec / 1e12, 5)})
+        log(f"cpu baseline {name} {extra[-1]['dtype']}: {sec * 1e3:.1f} ms per layer")
+    if extra:
+        out["legs"] = extra
+    return out
 
 
 def run_decode(args, hrm, dev):
@@ -260,8 +317,8 @@ def run_decode(args, hrm, dev):
                      "bytes_per_step": int(nbytes), "experts_touched": touched},
     }
     if not args.no_cpu_baseline:
-        cb = cpu_baseline(t, h, e, i, k, sample_tokens=t, runs=5)
-        result["cpu_baseline"] = {"value": round(cb["ms_per_layer_extrapolated"] * 1e3, 1), "unit": "us/layer",
+        cb = cpu_baseline(t, h, e, i, k, runs=5)
+        result["cpu_baseline"] = {"value": round(cb["ms_per_layer"] * 1e3, 1), "unit": "us/layer",
                                   "cores": cb["cores"], "kind": cb["kind"], "sample": cb["sample"]}
     print(json.dumps(result), flush=True)
 
@@ -320,6 +377,29 @@ def run_train_gemms(args, hrm, dev):
     }), flush=True)
 
 
+def _composition_compute(experts, hidden_states, selected_experts, routing_weights, dispatch=None):
+    """The reference's grouped composition (models/layers.py:311-334) under torch autograd, for comparison.
+
+    HIP router, dispatch and grouped GEMMs (hip_grouped_linear: forward, dgrad,
+    wgrad); gather, SwiGLU, weighting and index_add_ as torch ops.  Timed beside
+    the fused HIP backward of the expert block; not part of the package.
+    """
+    import torch.nn.functional as F
+    from hrm_moe_amd import hip_grouped_linear, ops
+
+    dtype = hidden_states.dtype
+    d = ops.permute(selected_experts, experts.num_experts, want_sort_idx=True)
+    tok = d.sorted_token_idx.long()
+    sorted_weights = routing_weights.to(dtype).reshape(-1).index_select(0, d.sort_idx)
+    gate_up = hip_grouped_linear(hidden_states.index_select(0, tok), experts.gate_up_weight.to(dtype),
+                                 d.tokens_per_expert)
+    gate, up = gate_up.chunk(2, dim=-1)
+    y = hip_grouped_linear(F.silu(gate) * up, experts.down_weight.to(dtype), d.tokens_per_expert)
+    out = torch.zeros_like(hidden_states)
+    out.index_add_(0, tok, (y * sorted_weights[:, None]).to(dtype))
+    return out, d.tokens_per_expert
+
+
 def run_layer_train(args, hrm, dev):
     """One training step of the whole MoE FFN layer: forward with the aux-loss context, then backward.
 
@@ -327,9 +407,11 @@ def run_layer_train(args, hrm, dev):
     the hidden states, the router weight and both expert weights.  Work per
     step counted: the expert GEMMs, 6*R*H*I forward + 12*R*H*I backward (dgrad
     and wgrad of both projections).  The same steps are also timed with the
-    reference's composition under autograd (fused_backward = False: torch ops
+    reference's composition under autograd (_composition_compute: torch ops
     for gather, SwiGLU, weighting and index_add_, HIP grouped GEMMs).
     """
+    import types
+
     t, h, e, i, k, bias = WORKLOADS[args.workload]
     r = t * k
     layers, xs = [], []
@@ -361,13 +443,14 @@ def run_layer_train(args, hrm, dev):
         torch.cuda.synchronize()
         return start.elapsed_time(end) / args.steps
 
-    ms = timed()
-    cls = type(layers[0].experts)
-    cls.fused_backward = False
+    for layer in layers:  # the composition first: it also settles the clocks before the timed fused steps
+        layer.experts._compute = types.MethodType(_composition_compute, layer.experts)
     try:
         ms_ref = timed()
     finally:
-        cls.fused_backward = True
+        for layer in layers:
+            del layer.experts._compute
+    ms = timed()
     flops = 18.0 * r * h * i
     tflops = flops / (ms * 1e-3) / 1e12
     log(f"{args.workload}: {ms:.4f} ms per training step ({tflops:.1f} TFLOP/s); "
@@ -394,6 +477,7 @@ def main():
     ap.add_argument("--workload", default="l64x8", choices=sorted(WORKLOADS))
     ap.add_argument("--weight-copies", type=int, default=2)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-cpu-legs", action="store_true", help="time only the bench's own layer on the CPU")
     ap.add_argument("--calibrate-copy-mb", type=int, default=0)
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -424,11 +508,15 @@ def main():
         layer, x = make_layer(hrm, dev, t, h, e, i, k, bias, seed=1234 + c)
         layers.append(layer)
         xs.append(x)
-    ms, wall = time_layers(layers, xs, args.steps, args.warmup)
-    # second pass over the same workload with HIP events around every op (on the op's stream)
+    # per-op pass first (HIP events around every op, on the op's stream); it also brings the
+    # clocks to their loaded state before the headline pass
+    from hrm_moe_amd import _lib
+
     timer = OpTimer(hrm.ops)
-    ms_instr, _ = time_layers(layers, xs, args.steps, 2, timer)
+    ms_instr, _ = time_layers(layers, xs, max(args.steps, 60), 2, timer)
     timer.restore()
+    gate_up_kernel = _lib.last_gemm_kernel(_lib.GEMM_KIND_GATE_UP)
+    ms, wall = time_layers(layers, xs, args.steps, args.warmup)
     flops = 6.0 * r * h * i
     tflops = flops / (ms * 1e-3) / 1e12
 
@@ -473,19 +561,29 @@ def main():
         "phase_ms": {n: round(v, 5) for n, v in phases.items()},
         "phase_pass_ms_per_layer": round(ms_instr, 5),
         "roofline": {
-            "kernel": "mgemm_dma_kernel<BF16, GATHER_SWIGLU, 128, 128, 2, 4, 64> (fused gather + gate_up GEMM + SwiGLU)",
+            "kernel": f"{gate_up_kernel} (fused gather + gate_up GEMM + SwiGLU)",
             "bound": "mfma",
             "achieved": round(achieved, 2),
             "peak": PEAK_BF16_TFLOPS,
             "unit": "TFLOP/s",
             "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
-            "traffic": read_traffic(f"gate_up_swiglu_{args.workload}_traffic.txt"),
+            "traffic": None,
             "flops_per_launch": gate_up_flops,
             "avg_launch_ms": round(gate_up_ms, 5),
         },
     }
+    traffic = read_traffic(f"gate_up_swiglu_{args.workload}_traffic.txt", gate_up_kernel)
+    if traffic is not None:
+        result["roofline"]["traffic"] = traffic["fetch_bytes_per_launch"] + traffic["write_bytes_per_launch"]
+        result["roofline"]["traffic_detail"] = traffic
     if not args.no_cpu_baseline:
-        result["cpu_baseline"] = cpu_baseline(t, h, e, i, k)
+        legs = []
+        if args.workload == "l64x8" and not args.no_cpu_legs:
+            xl = WORKLOADS["xl_skew"]
+            legs = [("l64x8", t, h, e, i, k, bias, torch.float32),
+                    ("xl_skew", xl[0], xl[1], xl[2], xl[3], xl[4], xl[5], torch.bfloat16),
+                    ("xl_skew", xl[0], xl[1], xl[2], xl[3], xl[4], xl[5], torch.float32)]
+        result["cpu_baseline"] = cpu_baseline(t, h, e, i, k, bias, legs=legs)
     print(json.dumps(result), flush=True)
 
 

@@ -38,6 +38,9 @@ _SZ = ctypes.c_size_t
 PROTOTYPES = {
     "hrm_moe_abi_version": (_INT, []),
     "hrm_moe_status_string": (ctypes.c_char_p, [_INT]),
+    "hrm_moe_reload_config": (_INT, []),
+    "hrm_moe_cu_margin": (_INT, []),
+    "hrm_moe_last_gemm_kernel": (ctypes.c_char_p, [_INT]),
     "hrm_moe_router_topk": (_INT, [_P, _INT, _I64, _I32, _I32, _I32, _P, _P, _P, _INT, _P]),
     "hrm_moe_permute_workspace_size": (_SZ, [_I64, _I32, _I32]),
     "hrm_moe_permute": (_INT, [_P, _I64, _I32, _I32, _P, _P, _P, _P, _P, _P, _SZ, _P]),
@@ -90,6 +93,19 @@ def load(path: str = LIB_PATH) -> ctypes.CDLL:
             raise RuntimeError(f"{path} has ABI version {version}, expected {ABI_VERSION}")
         _lib = lib
         return lib
+
+
+def reload_config() -> None:
+    """Make the library re-read its HRM_MOE_* tuning variables (tests switch kernel variants this way)."""
+    check(load().hrm_moe_reload_config(), "reload_config")
+
+
+GEMM_KIND_NT, GEMM_KIND_GATE_UP, GEMM_KIND_NN = 0, 1, 2
+
+
+def last_gemm_kernel(kind: int) -> str:
+    """Kernel instantiation of the latest grouped-GEMM launch of ``kind`` (a profiler kernel-name substring)."""
+    return load().hrm_moe_last_gemm_kernel(kind).decode()
 
 
 def status_string(status: int) -> str:

@@ -55,6 +55,23 @@ __device__ __forceinline__ void st8(void* p, u32x2 v) { *reinterpret_cast<u32x2*
 
 inline int ceil_div(int64_t a, int64_t b) { return int((a + b - 1) / b); }
 
+// Tuning knobs of the library, read from the environment on first use and
+// again by hrm_moe_reload_config().  Launchers read this snapshot, never the
+// environment itself.  Reloading while another thread launches is not safe.
+struct Config {
+  int cu_margin = 0;         // CUs left out of persistent grids (HRM_MOE_HIP_CU_MARGIN,
+                             // else HRM_MOE_TRITON_SM_MARGIN, else XTUNER_SM_MARGIN)
+  int gemm_bm = 0, gemm_bn = 0, gemm_stages = 0, gemm_waves = 4, gemm_bk = 64;  // HRM_MOE_GEMM_CFG, 0 = per call
+  int skinny = -1;           // HRM_MOE_SKINNY: -1 automatic, 0 off, 1 forced up to 16 rows per expert
+  int wgrad_stages = 0;      // HRM_MOE_WGRAD_STAGES: 0 automatic, 2 or 3 = 128 x 128 kernel with that ring
+  int64_t gate_split_rows = 1024;  // HRM_MOE_GATE_SPLIT_ROWS: rows per split of the gate weight gradient
+  bool wave_router = true;   // HRM_MOE_WAVE_ROUTER=0 turns the one-wave-per-token decode router off
+};
+const Config& config();
+// Re-reads the environment; returns HRM_MOE_OK, or HRM_MOE_ERR_INVALID when a
+// value is malformed (that knob then keeps its default).
+int reload_config();
+
 // Second dispatch stage (permute.hip), after a rank step that wrote rank[R] and
 // counts[nb][E+1] for rank blocks of SB slots: one scan + scatter launch.
 int dispatch_from_ranks(const int64_t* topk_idx, int64_t R, int E, int k, int SB, int nb, const int32_t* rank,

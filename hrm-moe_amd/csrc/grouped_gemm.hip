@@ -1620,28 +1620,33 @@ __global__ __launch_bounds__(kThreads, 1) void wgrad_dma_kernel(const uint16_t* 
 // ---------------------------------------------------------------------------
 constexpr int kBMMin = 128;  // smallest BM any launch uses (sizes the tile table)
 
-int cu_margin() {
-  static int margin = [] {
-    const char* s = getenv("HRM_MOE_HIP_CU_MARGIN");
-    int v = s ? atoi(s) : 0;
-    return v < 0 ? 0 : v;
-  }();
-  return margin;
-}
-
-// Persistent grid: (CUs - margin) x resident workgroups per CU, rounded down to a multiple of 8.
-template <typename KernelT>
-int persistent_grid(KernelT kernel, int threads = kThreads, size_t dyn_lds = 0) {
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess) return 8;
-  int cus = 0;
-  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus < 1) cus = 8;
-  int occ = 1;
-  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, kernel, threads, dyn_lds) != hipSuccess || occ < 1) occ = 1;
-  int g = (cus - cu_margin()) * occ;
-  g = (g / 8) * 8;
-  return g < 8 ? 8 : g;
-}
+// Persistent grid: (CUs - margin, at least 1) x resident workgroups per CU,
+// rounded down to a multiple of 8 (at least 8: the tile lists are split over
+// the 8 XCDs).  As the reference's grid of SM count - SM_MARGIN, at least 1
+// (models/moe_triton_grouped_gemm.py:50-52).  CU count and occupancy are
+// queried once per kernel (and LDS size); the margin is read per launch from
+// the library configuration.
+struct GridCache {
+  int cus = 0, occ = 0;
+  size_t lds = ~size_t(0);
+  template <typename KernelT>
+  int get(KernelT kernel, int threads = kThreads, size_t dyn_lds = 0) {
+    if (occ == 0 || lds != dyn_lds) {
+      int dev = 0, c = 0, o = 1;
+      if (hipGetDevice(&dev) != hipSuccess ||
+          hipDeviceGetAttribute(&c, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || c < 1)
+        c = 8;
+      if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&o, kernel, threads, dyn_lds) != hipSuccess || o < 1) o = 1;
+      cus = c;
+      occ = o;
+      lds = dyn_lds;
+    }
+    const int usable = cus - config().cu_margin;
+    int g = (usable < 1 ? 1 : usable) * occ;
+    g = (g / 8) * 8;
+    return g < 8 ? 8 : g;
+  }
+};
 
 int check_common(int64_t M, int32_t E, int dtype, const void* ws, size_t ws_bytes) {
   if (M < 0 || E < 1) return HRM_MOE_ERR_INVALID;
@@ -1650,6 +1655,13 @@ int check_common(int64_t M, int32_t E, int dtype, const void* ws, size_t ws_byte
   if (!ws || ws_bytes < gemm_ws_bytes(M, E, kBMMin)) return HRM_MOE_ERR_WORKSPACE;
   return HRM_MOE_OK;
 }
+
+// Name of the kernel instantiation the latest launch of each kind used, in
+// the form a profiler's demangled kernel name contains (for matching traces
+// and counter summaries to what ran).
+char g_last_kernel[3][128];
+template <typename TR>
+constexpr const char* tr_name() { return std::is_same<TR, BF16>::value ? "hrm::BF16" : "hrm::F16"; }
 
 template <typename TR, int KIND, int BM, int BN>
 int launch_mgemm(const void* A, const int32_t* gather, const void* W, const int64_t* tpe, int64_t M, int N, int K,
@@ -1660,8 +1672,10 @@ int launch_mgemm(const void* A, const int32_t* gather, const void* W, const int6
              w.work_counter);
   const int tiles_n = KIND == KIND_GATHER_SWIGLU ? (N + BN / 2 - 1) / (BN / 2) : (N + BN - 1) / BN;
   auto kern = mgemm_kernel<TR, KIND, BM, BN>;
-  static int grid = 0;
-  if (grid == 0) grid = persistent_grid(kern);
+  snprintf(g_last_kernel[KIND], sizeof(g_last_kernel[KIND]), "mgemm_kernel<%s, %d, %d, %d>", tr_name<TR>(), KIND, BM,
+           BN);
+  static GridCache gc;
+  const int grid = gc.get(kern);
   HRM_LAUNCH(kern, dim3(grid), dim3(kThreads), 0, stream, (const uint16_t*)A, gather, (const uint16_t*)W,
              (uint16_t*)C, w.tiles, w.count, N, K, tiles_n);
   return HRM_MOE_OK;
@@ -1673,12 +1687,11 @@ int launch_mgemm_dma(const void* A, const int32_t* gather, const void* W, const 
   (void)workspace;  // the DMA kernels plan their tiles themselves
   const int tiles_n = KIND == KIND_GATHER_SWIGLU ? (N + BN / 2 - 1) / (BN / 2) : (N + BN - 1) / BN;
   auto kern = mgemm_dma_kernel<TR, KIND, BM, BN, STAGES, NW, BK, EPI, WNT>;
+  snprintf(g_last_kernel[KIND], sizeof(g_last_kernel[KIND]), "mgemm_dma_kernel<%s, %d, %d, %d, %d, %d, %d, %d, %s>",
+           tr_name<TR>(), KIND, BM, BN, STAGES, NW, BK, EPI, WNT ? "true" : "false");
   const size_t plan_bytes = sizeof(int) * 3 * (size_t)E;
-  static int grid = 0, grid_e = -1;
-  if (grid == 0 || grid_e != E) {
-    grid = persistent_grid(kern, NW * 64, plan_bytes);
-    grid_e = E;
-  }
+  static GridCache gc;
+  const int grid = gc.get(kern, NW * 64, plan_bytes);
   HRM_LAUNCH(kern, dim3(grid), dim3(NW * 64), plan_bytes, stream, (const uint16_t*)A, gather, (const uint16_t*)W,
              (uint16_t*)C, tpe, E, (int)M, N, K, tiles_n, (uint32_t)(a_rows * K * 2), (uint16_t*)aux);
   return HRM_MOE_OK;
@@ -1709,11 +1722,10 @@ bool mcfg_built(const MCfg& c) {
   return false;
 }
 MCfg mgemm_cfg(int64_t M, int E, int64_t w_rows, bool gate_up, bool nn = false) {
-  const char* env = getenv("HRM_MOE_GEMM_CFG");  // read per call: tests switch variants in one process
-  if (env && *env) {
-    MCfg c{0, 0, 0, 4, 64};
-    const int n = sscanf(env, "%dx%dx%dx%dx%d", &c.bm, &c.bn, &c.stages, &c.waves, &c.bk);
-    if (n >= 3 && mcfg_built(c)) return c;
+  const Config& cf = config();  // HRM_MOE_GEMM_CFG (tests switch variants and reload the configuration)
+  if (cf.gemm_bm) {
+    const MCfg c{cf.gemm_bm, cf.gemm_bn, cf.gemm_stages, cf.gemm_waves, cf.gemm_bk};
+    if (mcfg_built(c)) return c;
   }
   // 256 x 256 tiles with 8 waves when experts average >= 256 rows and the
   // weight rows fill whole tiles (for the gate/up kernel: 2I a multiple of 256;
@@ -1754,8 +1766,7 @@ int dispatch_mgemm_t(const void* A, const int32_t* gather, const void* W, const 
   // HRM_MOE_SKINNY=1 forces it up to 16 rows per expert, =0 turns it off
   // (tests compare both paths).
   if constexpr (KIND != KIND_NN) {
-    const char* sk = getenv("HRM_MOE_SKINNY");
-    const bool force = sk && sk[0] == '1', off = sk && sk[0] == '0';
+    const bool force = config().skinny == 1, off = config().skinny == 0;
     const int64_t limit = force ? (int64_t)E * 16 : (int64_t)E / 4;
     const bool skinny_ok = !off && M <= limit && K % 32 == 0 && N % 16 == 0;
     if (skinny_ok) {
@@ -1766,7 +1777,10 @@ int dispatch_mgemm_t(const void* A, const int32_t* gather, const void* W, const 
 #define HRM_SK(NRB_)                                                                                          \
   HRM_LAUNCH((mgemm_skinny_kernel<TR, KIND, NRB_, 4>), grid, dim3(256), 0, stream, (const uint16_t*)A, gather, \
              (const uint16_t*)W, (uint16_t*)C, tpe, E, (int)M, N, K, cblk_n)
-      if (M <= (int64_t)E * 4) HRM_SK(1);  // up to 4 rows per expert on average: one 16-row block per pass
+      const int nrb = M <= (int64_t)E * 4 ? 1 : 2;  // up to 4 rows per expert on average: one 16-row block per pass
+      snprintf(g_last_kernel[KIND], sizeof(g_last_kernel[KIND]), "mgemm_skinny_kernel<%s, %d, %d, 4>", tr_name<TR>(),
+               KIND, nrb);
+      if (nrb == 1) HRM_SK(1);
       else HRM_SK(2);
 #undef HRM_SK
       return HRM_MOE_OK;
@@ -1855,8 +1869,8 @@ int launch_wgrad(const void* A, const void* B, const int64_t* tpe, int64_t M, in
   if (!dma) {
     if (gather) return HRM_MOE_ERR_UNSUPPORTED;  // operands beyond 32-bit buffer offsets
     auto kern = wgrad_kernel<TR, 128, 128>;
-    static int grid = 0;
-    if (grid == 0) grid = persistent_grid(kern);
+    static GridCache gc;
+    const int grid = gc.get(kern);
     HRM_LAUNCH(kern, dim3(grid), dim3(kThreads), 0, stream, (const uint16_t*)A, (const uint16_t*)B, (uint16_t*)C,
                w.row_offsets, E, Na, Nb, w.work_counter);
     return HRM_MOE_OK;
@@ -1864,41 +1878,40 @@ int launch_wgrad(const void* A, const void* B, const int64_t* tpe, int64_t M, in
   // 256 x 256 tiles with 8 waves when both widths fill them and experts have
   // enough rows to amortise a tile; HRM_MOE_WGRAD_STAGES=2|3 selects the
   // 128 x 128 four-wave kernel instead (gathered B: 2 stages).
-  const char* env = getenv("HRM_MOE_WGRAD_STAGES");  // read per call: tests switch kernels in one process
-  if (env && !*env) env = nullptr;
-  if (!env && Na >= 256 && Nb >= 256 && M >= (int64_t)E * 256) {
+  const int wstages = config().wgrad_stages;  // 0: automatic choice
+  if (wstages == 0 && Na >= 256 && Nb >= 256 && M >= (int64_t)E * 256) {
     if (gather) {
       auto kern = wgrad_dma8_kernel<TR, 256, 256, 8, 2, true>;
-      static int grid = 0;
-      if (grid == 0) grid = persistent_grid(kern, 512);
+      static GridCache gc;
+      const int grid = gc.get(kern, 512);
       HRM_LAUNCH(kern, dim3(grid), dim3(512), 0, stream, (const uint16_t*)A, (const uint16_t*)B, (uint16_t*)C,
                  w.row_offsets, E, Na, Nb, w.work_counter, b_index, b_bytes);
     } else {
       auto kern = wgrad_dma8_kernel<TR, 256, 256, 8, 2>;
-      static int grid = 0;
-      if (grid == 0) grid = persistent_grid(kern, 512);
+      static GridCache gc;
+      const int grid = gc.get(kern, 512);
       HRM_LAUNCH(kern, dim3(grid), dim3(512), 0, stream, (const uint16_t*)A, (const uint16_t*)B, (uint16_t*)C,
                  w.row_offsets, E, Na, Nb, w.work_counter, nullptr, 0u);
     }
     return HRM_MOE_OK;
   }
-  const int stages = gather || (env && atoi(env) == 2) ? 2 : 3;
+  const int stages = gather || wstages == 2 ? 2 : 3;
   if (gather) {
     auto kern = wgrad_dma_kernel<TR, 2, true>;
-    static int grid = 0;
-    if (grid == 0) grid = persistent_grid(kern);
+    static GridCache gc;
+    const int grid = gc.get(kern);
     HRM_LAUNCH(kern, dim3(grid), dim3(kThreads), 0, stream, (const uint16_t*)A, (const uint16_t*)B, (uint16_t*)C,
                w.row_offsets, E, Na, Nb, w.work_counter, b_index, b_bytes);
   } else if (stages == 2) {
     auto kern = wgrad_dma_kernel<TR, 2>;
-    static int grid = 0;
-    if (grid == 0) grid = persistent_grid(kern);
+    static GridCache gc;
+    const int grid = gc.get(kern);
     HRM_LAUNCH(kern, dim3(grid), dim3(kThreads), 0, stream, (const uint16_t*)A, (const uint16_t*)B, (uint16_t*)C,
                w.row_offsets, E, Na, Nb, w.work_counter, nullptr, 0u);
   } else {
     auto kern = wgrad_dma_kernel<TR, 3>;
-    static int grid = 0;
-    if (grid == 0) grid = persistent_grid(kern);
+    static GridCache gc;
+    const int grid = gc.get(kern);
     HRM_LAUNCH(kern, dim3(grid), dim3(kThreads), 0, stream, (const uint16_t*)A, (const uint16_t*)B, (uint16_t*)C,
                w.row_offsets, E, Na, Nb, w.work_counter, nullptr, 0u);
   }
@@ -1913,12 +1926,7 @@ int launch_wgrad(const void* A, const void* B, const int64_t* tpe, int64_t M, in
 // (torch's matmul: 101 us); short splits are dominated by each tile's pipeline
 // fill and epilogue, long ones leave CUs idle.
 inline int gate_wgrad_splits(int64_t T) {
-  static const int64_t rows = [] {
-    const char* env = getenv("HRM_MOE_GATE_SPLIT_ROWS");
-    const int64_t v = env ? atoll(env) : 1024;
-    return v < 64 ? int64_t(64) : v;
-  }();
-  int64_t s = T / rows;
+  int64_t s = T / config().gate_split_rows;
   return (int)(s < 1 ? 1 : (s > 128 ? 128 : s));
 }
 inline size_t gate_wgrad_ws_bytes(int64_t T, int E, int64_t H) {
@@ -1942,8 +1950,8 @@ int launch_gate_wgrad(const void* dlogits, const void* hidden, int64_t T, int E,
   HRM_LAUNCH(plan_kernel, dim3(1), dim3(1024), 0, stream, tpe, S, T, kBMMin, w.tiles, max_tiles, w.count,
              w.row_offsets, w.work_counter);
   auto kern = wgrad_dma_kernel<TR, 2, false, true>;
-  static int grid = 0;
-  if (grid == 0) grid = persistent_grid(kern);
+  static GridCache gc;
+  const int grid = gc.get(kern);
   HRM_LAUNCH(kern, dim3(grid), dim3(kThreads), 0, stream, (const uint16_t*)dlogits, (const uint16_t*)hidden,
              (uint16_t*)part, w.row_offsets, S, E, H, w.work_counter, nullptr, 0u);
   const int64_t n = (int64_t)E * H;
@@ -1954,6 +1962,11 @@ int launch_gate_wgrad(const void* dlogits, const void* hidden, int64_t T, int E,
 
 }  // namespace
 }  // namespace hrm
+
+extern "C" const char* hrm_moe_last_gemm_kernel(int kind) {
+  if (kind < 0 || kind > 2) return "";
+  return hrm::g_last_kernel[kind];
+}
 
 extern "C" size_t hrm_moe_gate_wgrad_workspace_size(int64_t num_tokens, int32_t num_experts, int64_t hidden_size) {
   if (num_tokens < 0 || num_experts < 1 || hidden_size < 1) return 0;

@@ -701,9 +701,8 @@ extern "C" int hrm_moe_router_topk_dispatch(const void* logits, int logits_dtype
     const bool solo = nb == 1;
     const hrm::DispatchOut dout{tokens_per_expert, expert_offsets, sorted_token_idx, sort_idx, slot_to_row};
     // up to 16 tokens and 64 experts: one wave per token (HRM_MOE_WAVE_ROUTER=0
-    // selects the quad kernel instead; read per call so tests can compare both)
-    const char* wr = getenv("HRM_MOE_WAVE_ROUTER");
-    if (num_tokens <= hrm::kWaveRouterMaxTokens && E <= 64 && !(wr && wr[0] == '0'))
+    // selects the quad kernel instead; tests compare both)
+    if (num_tokens <= hrm::kWaveRouterMaxTokens && E <= 64 && hrm::config().wave_router)
       return hrm::launch_router_dispatch_wave(logits, logits_dtype, num_tokens, E, k, norm_topk_prob, probs, topk_idx,
                                               topk_weight, weight_dtype, dout, stream);
     int st;

@@ -19,13 +19,17 @@ Deliberate difference: the reference runs a per-expert torch loop for CPU
 tensors (:481-482).  This op needs a ROCm GPU and raises RuntimeError for CPU
 tensors: it has no CPU path.
 
-The CU margin knob of the reference (HRM_MOE_TRITON_SM_MARGIN, fallback
-XTUNER_SM_MARGIN, :44-47) maps to HRM_MOE_HIP_CU_MARGIN: compute units left
-out of the persistent grids.
+The CU margin knob of the reference (HRM_MOE_TRITON_SM_MARGIN, falling back
+to XTUNER_SM_MARGIN, :24-52) is honoured under those names and under
+HRM_MOE_HIP_CU_MARGIN, which takes precedence: compute units left out of the
+persistent grids.  As in the reference, a value that is not a non-negative
+integer raises ValueError when this module is imported.  The kernel library
+reads the same variables (include/hrm_moe.h, hrm_moe_reload_config).
 """
 from __future__ import annotations
 
 import os
+import re
 
 import torch
 from torch import Tensor
@@ -33,11 +37,33 @@ from torch import Tensor
 from . import ops
 from .profile import record_moe_profile_phase
 
-if "HRM_MOE_HIP_CU_MARGIN" not in os.environ:
-    for _name in ("HRM_MOE_TRITON_SM_MARGIN", "XTUNER_SM_MARGIN"):
-        if os.environ.get(_name):
-            os.environ["HRM_MOE_HIP_CU_MARGIN"] = os.environ[_name]
-            break
+MARGIN_VARIABLES = ("HRM_MOE_HIP_CU_MARGIN", "HRM_MOE_TRITON_SM_MARGIN", "XTUNER_SM_MARGIN")
+_DECIMAL = re.compile(r"\s*[+-]?[0-9]+\s*")
+
+
+def cu_margin_from_env(environ=os.environ) -> int:
+    """CUs the persistent GEMM grids leave free: the first of MARGIN_VARIABLES that is set and non-empty.
+
+    Every variable that is set must hold a non-negative decimal integer, else
+    ValueError (the reference checks both of its names the same way,
+    models/moe_triton_grouped_gemm.py:33-47).
+    """
+    chosen = None
+    for name in MARGIN_VARIABLES:
+        raw = environ.get(name, "")
+        if raw == "":
+            continue
+        if not _DECIMAL.fullmatch(raw):
+            raise ValueError(f"{name} must be a non-negative integer, got {raw!r}")
+        value = int(raw)
+        if value < 0:
+            raise ValueError(f"{name} must be non-negative, got {value}")
+        if chosen is None:
+            chosen = value
+    return 0 if chosen is None else chosen
+
+
+CU_MARGIN = cu_margin_from_env()
 
 
 class _HipGroupedLinear(torch.autograd.Function):

@@ -9,17 +9,16 @@ Forward paths (same arithmetic, same routing bits):
   * no autograd needed (inference, ``torch.no_grad()``, or nothing requires
     grad): router kernel -> dispatch kernel -> fused gather + gate_up GEMM +
     SwiGLU -> down GEMM -> deterministic combine.  Five HIP launches plus the
-    gate GEMM; no host synchronisation.
-  * autograd needed, hidden size a multiple of 64: the same forward kernels
-    (the gate/up kernel also saving the rounded gate/up values) inside one
-    autograd function whose backward is HIP too: combine backward, down dgrad
-    with the SwiGLU backward fused, both wgrads, gate_up dgrad and a
-    deterministic un-permute.  The router's softmax/top-k backward is torch
-    ops on [T, E].
-  * autograd needed, other hidden sizes: the reference's grouped composition
-    (models/layers.py:311-334) with the HIP router, dispatch and grouped GEMMs
-    (forward, dgrad, wgrad); gather, SwiGLU, weighting and index_add_ are
-    torch ops under autograd.
+    gate GEMM; no host synchronisation.  Any hidden size that is a multiple
+    of 8.
+  * autograd needed: the same forward kernels (the gate/up kernel also saving
+    the rounded gate/up values) inside one autograd function whose backward
+    is HIP too: combine backward, down dgrad with the SwiGLU backward fused,
+    both wgrads, gate_up dgrad and a deterministic un-permute; the router's
+    softmax/top-k backward and the aux loss are HIP kernels as well.  The
+    fused training kernels stream hidden rows 64 values at a time, so this
+    path needs a hidden size that is a multiple of 64 and raises
+    NotImplementedError otherwise.
 """
 from __future__ import annotations
 
@@ -31,7 +30,6 @@ import torch.nn.functional as F
 from torch import Tensor, nn
 
 from . import ops
-from .grouped_gemm import hip_grouped_linear
 from .profile import record_moe_profile_phase
 
 
@@ -240,14 +238,10 @@ class SparseMoEGroupedExperts(nn.Module):
 
     Parameters: ``gate_up_weight`` [E, 2I, H] (gate rows 0..I-1, up rows
     I..2I-1) and ``down_weight`` [E, H, I].
-
-    ``fused_backward`` (default True) selects the HIP backward of the whole
-    expert block when autograd is needed and the hidden size is a multiple of
-    64; False runs the reference's composition under autograd instead (same
-    forward values; used to compare the two).
     """
 
-    fused_backward = True
+    # hidden sizes the fused training kernels accept (they stream K 64 values at a time)
+    TRAIN_HIDDEN_MULTIPLE = 64
 
     def __init__(self, hidden_size: int, intermediate_size: int, num_experts: int, backend: str = "hip",
                  init_std_in=None, init_std_out=None, **kwargs):
@@ -281,8 +275,7 @@ class SparseMoEGroupedExperts(nn.Module):
         """(expert output [T,H], tokens_per_expert [E] int64 from the dispatch, or None when T == 0).
 
         ``dispatch``: the permutation of ``selected_experts`` when the caller
-        already has it (the router's fused dispatch); the reference-composition
-        path (which needs ``sort_idx``) computes its own.
+        already has it (the router's fused dispatch).
         """
         num_tokens = hidden_states.shape[0]
         dtype = hidden_states.dtype
@@ -302,32 +295,15 @@ class SparseMoEGroupedExperts(nn.Module):
             with record_moe_profile_phase("combine"):
                 return ops.combine(y, d, routing_weights), d.tokens_per_expert
 
-        if self.fused_backward and hidden_states.shape[1] % 64 == 0:
-            # HIP forward and backward of the whole expert block
-            with record_moe_profile_phase("dispatch"):
-                d = dispatch if dispatch is not None else ops.permute(selected_experts, self.num_experts)
-            with record_moe_profile_phase("experts"):
-                out = _GroupedExpertsFn.apply(hidden_states, routing_weights, gate_up_weight, down_weight, d)
-            return out, d.tokens_per_expert
-
-        # hidden sizes that are not a multiple of 64: the reference's composition,
-        # with the HIP grouped GEMMs under torch autograd
+        if hidden_states.shape[1] % self.TRAIN_HIDDEN_MULTIPLE != 0:
+            raise NotImplementedError(
+                f"training the MoE FFN needs a hidden size that is a multiple of {self.TRAIN_HIDDEN_MULTIPLE} "
+                f"(got {hidden_states.shape[1]}); the forward without autograd accepts multiples of 8")
+        # HIP forward and backward of the whole expert block
         with record_moe_profile_phase("dispatch"):
-            d = ops.permute(selected_experts, self.num_experts, want_sort_idx=True)
-            sorted_token_idx = d.sorted_token_idx.long()
-            sorted_weights = routing_weights.reshape(-1).index_select(0, d.sort_idx)
-            sorted_hidden_states = hidden_states.index_select(0, sorted_token_idx)
-        with record_moe_profile_phase("gate_up_gemm"):
-            gate_up = hip_grouped_linear(sorted_hidden_states, gate_up_weight, d.tokens_per_expert)
-        with record_moe_profile_phase("activation"):
-            gate, up = gate_up.chunk(2, dim=-1)
-            activated = F.silu(gate) * up
-        with record_moe_profile_phase("down_gemm"):
-            expert_output = hip_grouped_linear(activated, down_weight, d.tokens_per_expert)
-        with record_moe_profile_phase("combine"):
-            expert_output = expert_output * sorted_weights[:, None]
-            out = torch.zeros_like(hidden_states)
-            out.index_add_(0, sorted_token_idx, expert_output.to(dtype))
+            d = dispatch if dispatch is not None else ops.permute(selected_experts, self.num_experts)
+        with record_moe_profile_phase("experts"):
+            out = _GroupedExpertsFn.apply(hidden_states, routing_weights, gate_up_weight, down_weight, d)
         return out, d.tokens_per_expert
 
     def forward(self, hidden_states: Tensor, selected_experts: Tensor, routing_weights: Tensor,

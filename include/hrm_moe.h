@@ -48,6 +48,37 @@ int hrm_moe_abi_version(void);
 const char* hrm_moe_status_string(int status);
 
 /*
+ * Tuning configuration.  The library reads its knobs from the environment on
+ * first use and keeps that snapshot; launches never read the environment.
+ * hrm_moe_reload_config() reads it again (not safe while another thread
+ * launches).  Returns HRM_MOE_OK, or HRM_MOE_ERR_INVALID when a value is
+ * malformed (that knob keeps its default).
+ *   HRM_MOE_HIP_CU_MARGIN, else HRM_MOE_TRITON_SM_MARGIN, else XTUNER_SM_MARGIN:
+ *       compute units left out of the persistent GEMM grids, a non-negative
+ *       integer.  Replaces SM_MARGIN of models/moe_triton_grouped_gemm.py:24-52
+ *       (grid = max(1, SMs - margin)); here grid = max(1, CUs - margin) x
+ *       workgroups per CU, rounded down to a multiple of 8, at least 8.
+ *   HRM_MOE_GEMM_CFG, HRM_MOE_SKINNY, HRM_MOE_WGRAD_STAGES,
+ *   HRM_MOE_GATE_SPLIT_ROWS, HRM_MOE_WAVE_ROUTER: kernel and tile choices
+ *       (tests and tuning), replacing the reference's BLOCK_M / autotune knobs
+ *       (models/moe_triton_grouped_gemm.py:48,70-110).
+ */
+int hrm_moe_reload_config(void);
+/* The CU margin of the current configuration. */
+int hrm_moe_cu_margin(void);
+
+/*
+ * Diagnostic, with no counterpart in the reference: the kernel instantiation
+ * the latest M-grouped GEMM launch of `kind` used (0 = NT, the down
+ * projection and forward grouped linear; 1 = gather + gate_up + SwiGLU;
+ * 2 = NN, dgrad), as it appears inside a profiler's demangled kernel name,
+ * e.g. "mgemm_dma_kernel<hrm::BF16, 1, 128, 128, 2, 4, 64, 0, false>".
+ * Empty before the first launch of that kind.  Lets a benchmark check that a
+ * counter summary describes the kernel it timed.
+ */
+const char* hrm_moe_last_gemm_kernel(int kind);
+
+/*
  * Router: fp32 softmax over experts, top-k, optional renormalisation, cast.
  * Replaces models/layers.py:606-610:
  *   probs = F.softmax(logits, -1, dtype=float32); w, idx = torch.topk(probs, k)

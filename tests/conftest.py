@@ -1,3 +1,4 @@
+import contextlib
 import os
 import sys
 
@@ -29,3 +30,26 @@ def cuda():
 
     hrm_moe_amd.load_library()
     return torch.device("cuda:0")
+
+
+@contextlib.contextmanager
+def lib_env(**values):
+    """Set HRM_MOE_* tuning variables (None = unset), reload the library's configuration, restore both after."""
+    from hrm_moe_amd import _lib
+
+    saved = {n: os.environ.get(n) for n in values}
+    try:
+        for n, v in values.items():
+            if v is None:
+                os.environ.pop(n, None)
+            else:
+                os.environ[n] = v
+        _lib.reload_config()
+        yield
+    finally:
+        for n, v in saved.items():
+            if v is None:
+                os.environ.pop(n, None)
+            else:
+                os.environ[n] = v
+        _lib.reload_config()

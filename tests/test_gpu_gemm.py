@@ -17,6 +17,7 @@ import hrm_moe_amd
 from hrm_moe_amd import ops
 from oracle import moe_oracle as mo
 from oracle import synth
+from conftest import lib_env
 
 pytestmark = pytest.mark.gpu
 
@@ -128,22 +129,14 @@ GATHER_TN_CASES = [
 @pytest.mark.parametrize("m,na,nb,e,b_rows,dtype,kernel", GATHER_TN_CASES)
 def test_grouped_gemm_tn_gather(cuda, m, na, nb, e, b_rows, dtype, kernel):
     """Gathered B rows give exactly the wgrad over the materialised rows (same accumulation order)."""
-    import os
     tpe = make_tpe("ragged", m + nb, m, e)
     g = torch.from_numpy(synth.normal(m + 5, (m, na))).to(dtype).to(cuda)
     b = torch.from_numpy(synth.normal(m + 6, (b_rows, nb))).to(dtype).to(cuda)
     idx = torch.from_numpy(np.random.default_rng(m).integers(0, b_rows, size=m)).to(torch.int32).to(cuda)
     tpe_d = torch.from_numpy(tpe).to(cuda)
-    old = os.environ.get("HRM_MOE_WGRAD_STAGES")
-    os.environ["HRM_MOE_WGRAD_STAGES"] = kernel
-    try:
+    with lib_env(HRM_MOE_WGRAD_STAGES=kernel):
         got = ops.grouped_gemm_tn_gather(g, b, idx, tpe_d)
         want = ops.grouped_gemm_tn(g, b.index_select(0, idx.long()), tpe_d)
-    finally:
-        if old is None:
-            os.environ.pop("HRM_MOE_WGRAD_STAGES", None)
-        else:
-            os.environ["HRM_MOE_WGRAD_STAGES"] = old
     assert torch.equal(got, want)
     ref = mo.grouped_linear_wgrad(g.cpu(), b.cpu().index_select(0, idx.cpu().long()), tpe, num_experts=e)
     close(got, ref, f"tn_gather {m}x{na}x{nb} e{e}")
@@ -185,19 +178,19 @@ EDGE_TPE = np.array([1, 31, 32, 33, 0, 63, 64, 65, 95, 96, 97, 127, 128, 129, 0,
 
 
 @pytest.mark.parametrize("cfg", ["", "128x128x2x4x64", "256x256x2x8x64"])
-def test_grouped_gemm_row_block_edges(cuda, monkeypatch, cfg):
-    monkeypatch.setenv("HRM_MOE_GEMM_CFG", cfg)
+def test_grouped_gemm_row_block_edges(cuda, cfg):
     e, m = EDGE_TPE.size, int(EDGE_TPE.sum())
     n, k = 512, 448
     tpe = torch.from_numpy(EDGE_TPE).to(cuda)
     a = torch.from_numpy(synth.normal(11, (m, k))).to(torch.bfloat16)
     w = torch.from_numpy(synth.normal(12, (e, n, k), std=0.05)).to(torch.bfloat16)
-    got = ops.grouped_gemm_nt(a.to(cuda), w.to(cuda), tpe)
-    close(got, mo.grouped_linear(a, w, EDGE_TPE), f"nt edges {cfg}")
     g = torch.from_numpy(synth.normal(13, (m, n))).to(torch.bfloat16)
-    dg = ops.grouped_gemm_nn(g.to(cuda), w.to(cuda), tpe)
+    with lib_env(HRM_MOE_GEMM_CFG=cfg):
+        got = ops.grouped_gemm_nt(a.to(cuda), w.to(cuda), tpe)
+        dg = ops.grouped_gemm_nn(g.to(cuda), w.to(cuda), tpe)
+    close(got, mo.grouped_linear(a, w, EDGE_TPE), f"nt edges {cfg}")
     close(dg, mo.grouped_linear_dgrad(g, w, EDGE_TPE), f"nn edges {cfg}")
     # the tile shapes accumulate K in the same order: identical bits
-    monkeypatch.setenv("HRM_MOE_GEMM_CFG", "128x128x2x4x64")
-    assert torch.equal(got, ops.grouped_gemm_nt(a.to(cuda), w.to(cuda), tpe))
-    assert torch.equal(dg, ops.grouped_gemm_nn(g.to(cuda), w.to(cuda), tpe))
+    with lib_env(HRM_MOE_GEMM_CFG="128x128x2x4x64"):
+        assert torch.equal(got, ops.grouped_gemm_nt(a.to(cuda), w.to(cuda), tpe))
+        assert torch.equal(dg, ops.grouped_gemm_nn(g.to(cuda), w.to(cuda), tpe))

@@ -12,14 +12,13 @@ multiple of 64.  All of them accumulate each output over K in the same order
 default choice, which the oracle checks elsewhere (test_gpu_gemm.py,
 test_gpu_layer.py).  HRM_MOE_GEMM_CFG selects the variant per call.
 """
-import os
-
 import numpy as np
 import pytest
 import torch
 
 from hrm_moe_amd import ops
 from oracle import synth
+from conftest import lib_env
 
 pytestmark = pytest.mark.gpu
 
@@ -38,17 +37,10 @@ def _ragged(seed, m, e):
 
 def _run_all(fn):
     out = {}
-    old = os.environ.get("HRM_MOE_GEMM_CFG")
-    try:
-        for v in [""] + VARIANTS:
-            os.environ["HRM_MOE_GEMM_CFG"] = v
+    for v in [""] + VARIANTS:
+        with lib_env(HRM_MOE_GEMM_CFG=v):
             out[v or "default"] = fn()
             torch.cuda.synchronize()
-    finally:
-        if old is None:
-            os.environ.pop("HRM_MOE_GEMM_CFG", None)
-        else:
-            os.environ["HRM_MOE_GEMM_CFG"] = old
     return out
 
 
@@ -84,17 +76,10 @@ def test_nt_nn_variants_identical(cuda, m, n, kk, e):
 
 def _run_wgrad(fn):
     out = {}
-    old = os.environ.get("HRM_MOE_WGRAD_STAGES")
-    try:
-        for v in ["", "2", "3"]:
-            os.environ["HRM_MOE_WGRAD_STAGES"] = v
+    for v in ["", "2", "3"]:
+        with lib_env(HRM_MOE_WGRAD_STAGES=v):
             out[v or "default"] = fn()
             torch.cuda.synchronize()
-    finally:
-        if old is None:
-            os.environ.pop("HRM_MOE_WGRAD_STAGES", None)
-        else:
-            os.environ["HRM_MOE_WGRAD_STAGES"] = old
     return out
 
 

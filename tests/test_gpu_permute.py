@@ -11,6 +11,7 @@ import torch
 
 from hrm_moe_amd import ops
 from oracle import moe_oracle as mo
+from conftest import lib_env
 
 pytestmark = pytest.mark.gpu
 
@@ -115,17 +116,17 @@ def test_router_dispatch_zero_tokens(cuda):
     (17, 64, 8, torch.bfloat16, torch.bfloat16, True, 0), (64, 64, 8, torch.bfloat16, torch.bfloat16, True, 0),
     (50, 40, 5, torch.float32, torch.float16, True, 0), (64, 64, 8, torch.bfloat16, torch.bfloat16, True, 3),
     (33, 8, 2, torch.bfloat16, torch.bfloat16, False, 2), (63, 64, 7, torch.bfloat16, torch.float32, True, 5)])
-def test_router_dispatch_decode_sizes(cuda, monkeypatch, wave, t, e, k, ldt, wdt, norm, levels):
+def test_router_dispatch_decode_sizes(cuda, wave, t, e, k, ldt, wdt, norm, levels):
     """Up to 64 tokens (the wave-per-token kernel up to 16, the quad kernel in both settings above) give the bits of
     router_topk followed by permute, ties included; the indices and weights also equal torch's on the device."""
-    monkeypatch.setenv("HRM_MOE_WAVE_ROUTER", wave)
     rng = np.random.default_rng(1000 * t + 10 * e + k + levels)
     if levels:
         z = rng.integers(0, levels, size=(t, e)).astype(np.float32) * 0.25
     else:
         z = rng.standard_normal((t, e)).astype(np.float32)
     lg = torch.from_numpy(z).to(ldt).to(cuda)
-    probs, w, idx, d = ops.router_topk_dispatch(lg, k, norm, wdt, want_probs=True, want_sort_idx=True)
+    with lib_env(HRM_MOE_WAVE_ROUTER=wave):
+        probs, w, idx, d = ops.router_topk_dispatch(lg, k, norm, wdt, want_probs=True, want_sort_idx=True)
     probs2, w2, idx2 = ops.router_topk(lg, k, norm, wdt)
     d2 = ops.permute(idx2, e, want_sort_idx=True)
     assert torch.equal(idx, idx2) and torch.equal(w.view(-1).float(), w2.view(-1).float())

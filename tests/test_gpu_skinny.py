@@ -7,8 +7,6 @@ all covered at the L and XL shapes.  Bar as for the other grouped GEMMs:
 max|d| <= 1e-2 max|ref|, mean|d| <= 2e-3 mean|ref|.  HRM_MOE_SKINNY=0 forces
 the tiled kernels for the same call, which must agree to the same bar.
 """
-import os
-
 import numpy as np
 import pytest
 import torch
@@ -16,6 +14,7 @@ import torch
 from hrm_moe_amd import ops
 from oracle import moe_oracle as mo
 from oracle import synth
+from conftest import lib_env
 
 pytestmark = pytest.mark.gpu
 
@@ -40,15 +39,8 @@ def skewed_tpe(seed, m, e):
 
 
 def _with_skinny(flag, fn):
-    old = os.environ.get("HRM_MOE_SKINNY")
-    os.environ["HRM_MOE_SKINNY"] = flag
-    try:
+    with lib_env(HRM_MOE_SKINNY=flag):
         return fn()
-    finally:
-        if old is None:
-            os.environ.pop("HRM_MOE_SKINNY", None)
-        else:
-            os.environ["HRM_MOE_SKINNY"] = old
 
 
 def _tiled(fn):

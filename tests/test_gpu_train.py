@@ -9,8 +9,6 @@ are bit-exact (one rounded product each); everything that sums (d_w, the
 dgrad, the wgrads) is within bf16 tolerance of the oracle:
 max|got - ref| <= 2e-2 * max|ref| with the mean absolute error printed.
 """
-import os
-
 import numpy as np
 import pytest
 import torch
@@ -20,6 +18,7 @@ from hrm_moe_amd import ops
 from hrm_moe_amd.layers import _GroupedExpertsFn
 from oracle import moe_oracle as mo
 from oracle import synth
+from conftest import lib_env
 
 pytestmark = pytest.mark.gpu
 BF = torch.bfloat16
@@ -56,17 +55,10 @@ def test_gate_up_save_is_bit_identical(cuda, cfg, seed, t, h, e, i, k, bias):
     x, w, idx, wgu, wdn, _ = _case(seed, t, h, e, i, k, bias)
     xg, wgug = x.to(cuda), wgu.to(cuda)
     d = ops.permute(idx.to(cuda), e)
-    old = os.environ.get("HRM_MOE_GEMM_CFG")
-    os.environ["HRM_MOE_GEMM_CFG"] = cfg
-    try:
+    with lib_env(HRM_MOE_GEMM_CFG=cfg):
         act, gate_up = ops.gate_up_swiglu_save(xg, d, wgug)
         act_plain = ops.gate_up_swiglu(xg, d, wgug)
         gu_plain = ops.grouped_gemm_nt(xg.index_select(0, d.sorted_token_idx.long()), wgug, d.tokens_per_expert)
-    finally:
-        if old is None:
-            os.environ.pop("HRM_MOE_GEMM_CFG", None)
-        else:
-            os.environ["HRM_MOE_GEMM_CFG"] = old
     assert torch.equal(act, act_plain), "act"
     assert torch.equal(gate_up, gu_plain), "gate_up"
     ref = mo.experts_vjp(x, w, wgu, wdn, idx.numpy(), torch.zeros(t, h, dtype=BF))
