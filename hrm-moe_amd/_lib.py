@@ -56,6 +56,9 @@ PROTOTYPES = {
     "hrm_moe_router_dispatch_workspace_size": (_SZ, [_I64, _I32, _I32]),
     "hrm_moe_router_topk_dispatch": (_INT, [_P, _INT, _I64, _I32, _I32, _I32, _P, _P, _P, _INT, _P, _P, _P, _P, _P,
                                             _P, _SZ, _P]),
+    "hrm_moe_router_dispatch_noalloc_max_bytes": (_SZ, []),
+    "hrm_moe_router_topk_dispatch_noalloc": (_INT, [_P, _INT, _I64, _I32, _I32, _I32, _P, _P, _P, _INT, _P, _P, _P,
+                                                    _P, _P, _P]),
     "hrm_moe_gate_wgrad_workspace_size": (_SZ, [_I64, _I32, _I64]),
     "hrm_moe_gate_wgrad": (_INT, [_P, _P, _I64, _I32, _I64, _INT, _P, _P, _SZ, _P]),
     "hrm_moe_router_topk_backward": (_INT, [_P, _P, _P, _INT, _P, _I64, _I64, _I32, _I32, _I32, _P, _INT, _P]),

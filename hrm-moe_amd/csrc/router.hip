@@ -26,6 +26,8 @@
 //    order and weight-sum order from topk_order.h.
 #include <stdlib.h>
 
+#include <mutex>
+
 #include "common.h"
 #include "topk_order.h"
 
@@ -674,12 +676,13 @@ extern "C" size_t hrm_moe_router_dispatch_workspace_size(int64_t num_tokens, int
   return hrm::router_dispatch_ws(num_tokens, num_experts, top_k);
 }
 
-extern "C" int hrm_moe_router_topk_dispatch(const void* logits, int logits_dtype, int64_t num_tokens,
-                                            int32_t num_experts, int32_t top_k, int32_t norm_topk_prob, float* probs,
-                                            int64_t* topk_idx, void* topk_weight, int weight_dtype,
-                                            int64_t* tokens_per_expert, int32_t* expert_offsets,
-                                            int32_t* sorted_token_idx, int64_t* sort_idx, int32_t* slot_to_row,
-                                            void* workspace, size_t workspace_bytes, void* stream) {
+namespace hrm {
+namespace {
+
+int check_router_dispatch(const void* logits, int logits_dtype, int64_t num_tokens, int32_t num_experts,
+                          int32_t top_k, const int64_t* topk_idx, const void* topk_weight, int weight_dtype,
+                          const int64_t* tokens_per_expert, const int32_t* expert_offsets,
+                          const int32_t* sorted_token_idx, const int32_t* slot_to_row) {
   if (num_tokens < 0 || num_experts < 1 || top_k < 1 || top_k > num_experts) return HRM_MOE_ERR_INVALID;
   if (logits_dtype < HRM_MOE_BF16 || logits_dtype > HRM_MOE_F32) return HRM_MOE_ERR_DTYPE;
   if (weight_dtype < HRM_MOE_BF16 || weight_dtype > HRM_MOE_F32) return HRM_MOE_ERR_DTYPE;
@@ -687,11 +690,19 @@ extern "C" int hrm_moe_router_topk_dispatch(const void* logits, int logits_dtype
   if (!tokens_per_expert || !expert_offsets) return HRM_MOE_ERR_INVALID;
   if (num_tokens > 0 && (!logits || !topk_idx || !topk_weight || !sorted_token_idx || !slot_to_row))
     return HRM_MOE_ERR_INVALID;
-  if (!workspace || workspace_bytes < hrm::router_dispatch_ws(num_tokens, num_experts, top_k))
-    return HRM_MOE_ERR_WORKSPACE;
+  return HRM_MOE_OK;
+}
+
+// Router + dispatch over a scratch area of at least router_dispatch_ws bytes:
+// rank[T*k] and counts[nb][E+1].  The rank step writes every entry of both
+// that the scan + scatter launch reads, so the scratch need not start zeroed.
+int router_dispatch(const void* logits, int logits_dtype, int64_t num_tokens, int32_t num_experts, int32_t top_k,
+                    int32_t norm_topk_prob, float* probs, int64_t* topk_idx, void* topk_weight, int weight_dtype,
+                    int64_t* tokens_per_expert, int32_t* expert_offsets, int32_t* sorted_token_idx,
+                    int64_t* sort_idx, int32_t* slot_to_row, void* workspace, void* stream) {
   const int E = num_experts, k = top_k;
   const int64_t R = num_tokens * k;
-  const int nb = (int)hrm::router_dispatch_blocks(num_tokens);
+  const int nb = (int)router_dispatch_blocks(num_tokens);
   char* p = static_cast<char*>(workspace);
   int32_t* rank = reinterpret_cast<int32_t*>(p);
   p += (sizeof(int32_t) * (size_t)R + 255) & ~size_t(255);
@@ -699,25 +710,98 @@ extern "C" int hrm_moe_router_topk_dispatch(const void* logits, int logits_dtype
   if (num_tokens > 0) {
     // up to 64 tokens: one router block finishes the dispatch itself (no second launch)
     const bool solo = nb == 1;
-    const hrm::DispatchOut dout{tokens_per_expert, expert_offsets, sorted_token_idx, sort_idx, slot_to_row};
+    const DispatchOut dout{tokens_per_expert, expert_offsets, sorted_token_idx, sort_idx, slot_to_row};
     // up to 16 tokens and 64 experts: one wave per token (HRM_MOE_WAVE_ROUTER=0
     // selects the quad kernel instead; tests compare both)
-    if (num_tokens <= hrm::kWaveRouterMaxTokens && E <= 64 && hrm::config().wave_router)
-      return hrm::launch_router_dispatch_wave(logits, logits_dtype, num_tokens, E, k, norm_topk_prob, probs, topk_idx,
-                                              topk_weight, weight_dtype, dout, stream);
+    if (num_tokens <= kWaveRouterMaxTokens && E <= 64 && config().wave_router)
+      return launch_router_dispatch_wave(logits, logits_dtype, num_tokens, E, k, norm_topk_prob, probs, topk_idx,
+                                         topk_weight, weight_dtype, dout, stream);
     int st;
     if (E <= 8)
-      st = hrm::launch_router_rank<8>(logits, logits_dtype, num_tokens, E, k, norm_topk_prob, probs, topk_idx,
-                                      topk_weight, weight_dtype, rank, counts, dout, solo, stream);
+      st = launch_router_rank<8>(logits, logits_dtype, num_tokens, E, k, norm_topk_prob, probs, topk_idx,
+                                 topk_weight, weight_dtype, rank, counts, dout, solo, stream);
     else if (E <= 64)
-      st = hrm::launch_router_rank<64>(logits, logits_dtype, num_tokens, E, k, norm_topk_prob, probs, topk_idx,
-                                       topk_weight, weight_dtype, rank, counts, dout, solo, stream);
+      st = launch_router_rank<64>(logits, logits_dtype, num_tokens, E, k, norm_topk_prob, probs, topk_idx,
+                                  topk_weight, weight_dtype, rank, counts, dout, solo, stream);
     else
-      st = hrm::launch_router_rank<128>(logits, logits_dtype, num_tokens, E, k, norm_topk_prob, probs, topk_idx,
-                                        topk_weight, weight_dtype, rank, counts, dout, solo, stream);
+      st = launch_router_rank<128>(logits, logits_dtype, num_tokens, E, k, norm_topk_prob, probs, topk_idx,
+                                   topk_weight, weight_dtype, rank, counts, dout, solo, stream);
     if (st) return st;
     if (solo) return HRM_MOE_OK;
   }
-  return hrm::dispatch_from_ranks(topk_idx, R, E, k, 64 * k, nb, rank, counts, tokens_per_expert, expert_offsets,
-                                  sorted_token_idx, sort_idx, slot_to_row, stream);
+  return dispatch_from_ranks(topk_idx, R, E, k, 64 * k, nb, rank, counts, tokens_per_expert, expert_offsets,
+                             sorted_token_idx, sort_idx, slot_to_row, stream);
+}
+
+// The no-allocation entry point's scratch: rank[T*k] and counts[nb][E+1] for
+// up to 32768 tokens at E <= 128 and k <= 8 (1.25 MiB).  Each GPU the library
+// runs on holds its own copy until the process ends.  In host code the array's
+// name is not a device address: set-up takes each device's address with
+// hipGetSymbolAddress and only that address is passed on.
+constexpr size_t kScratchBytes = ((sizeof(int32_t) * 32768 * 8 + 255) & ~size_t(255)) +
+                                 ((sizeof(int32_t) * ((32768 + 63) / 64) * (128 + 1) + 255) & ~size_t(255)) + 256;
+}  // namespace
+__device__ __align__(256) char scratch[kScratchBytes];
+namespace {
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mutex;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+// This device's address of `scratch` (looked up once per device, with the device current).
+int scratch_for_current_device(void** out) {
+  int dev = 0;
+  hipError_t err = hipGetDevice(&dev);
+  if (err != hipSuccess) return (int)err;
+  if (dev < 0 || dev >= kMaxDevices) return HRM_MOE_ERR_UNSUPPORTED;
+  std::lock_guard<std::mutex> lock(g_scratch_mutex);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    err = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (err != hipSuccess) return (int)err;
+    if (!p) return HRM_MOE_ERR_INVALID;
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return HRM_MOE_OK;
+}
+
+}  // namespace
+}  // namespace hrm
+
+extern "C" int hrm_moe_router_topk_dispatch(const void* logits, int logits_dtype, int64_t num_tokens,
+                                            int32_t num_experts, int32_t top_k, int32_t norm_topk_prob, float* probs,
+                                            int64_t* topk_idx, void* topk_weight, int weight_dtype,
+                                            int64_t* tokens_per_expert, int32_t* expert_offsets,
+                                            int32_t* sorted_token_idx, int64_t* sort_idx, int32_t* slot_to_row,
+                                            void* workspace, size_t workspace_bytes, void* stream) {
+  const int st = hrm::check_router_dispatch(logits, logits_dtype, num_tokens, num_experts, top_k, topk_idx,
+                                            topk_weight, weight_dtype, tokens_per_expert, expert_offsets,
+                                            sorted_token_idx, slot_to_row);
+  if (st) return st;
+  if (!workspace || workspace_bytes < hrm::router_dispatch_ws(num_tokens, num_experts, top_k))
+    return HRM_MOE_ERR_WORKSPACE;
+  return hrm::router_dispatch(logits, logits_dtype, num_tokens, num_experts, top_k, norm_topk_prob, probs, topk_idx,
+                              topk_weight, weight_dtype, tokens_per_expert, expert_offsets, sorted_token_idx,
+                              sort_idx, slot_to_row, workspace, stream);
+}
+
+extern "C" size_t hrm_moe_router_dispatch_noalloc_max_bytes(void) { return hrm::kScratchBytes; }
+
+extern "C" int hrm_moe_router_topk_dispatch_noalloc(const void* logits, int logits_dtype, int64_t num_tokens,
+                                                    int32_t num_experts, int32_t top_k, int32_t norm_topk_prob,
+                                                    float* probs, int64_t* topk_idx, void* topk_weight,
+                                                    int weight_dtype, int64_t* tokens_per_expert,
+                                                    int32_t* expert_offsets, int32_t* sorted_token_idx,
+                                                    int64_t* sort_idx, int32_t* slot_to_row, void* stream) {
+  int st = hrm::check_router_dispatch(logits, logits_dtype, num_tokens, num_experts, top_k, topk_idx, topk_weight,
+                                      weight_dtype, tokens_per_expert, expert_offsets, sorted_token_idx, slot_to_row);
+  if (st) return st;
+  if (hrm::router_dispatch_ws(num_tokens, num_experts, top_k) > hrm::kScratchBytes) return HRM_MOE_ERR_UNSUPPORTED;
+  void* ws = nullptr;
+  st = hrm::scratch_for_current_device(&ws);
+  if (st) return st;
+  return hrm::router_dispatch(logits, logits_dtype, num_tokens, num_experts, top_k, norm_topk_prob, probs, topk_idx,
+                              topk_weight, weight_dtype, tokens_per_expert, expert_offsets, sorted_token_idx,
+                              sort_idx, slot_to_row, ws, stream);
 }

@@ -136,6 +136,29 @@ int hrm_moe_router_topk_dispatch(const void* logits, int logits_dtype, int64_t n
                                  int32_t* slot_to_row, void* workspace, size_t workspace_bytes, void* stream);
 
 /*
+ * hrm_moe_router_topk_dispatch without a workspace argument: same arguments
+ * (minus workspace and workspace_bytes), same outputs, same limits.  No
+ * counterpart in the reference: it is for callers that cannot allocate
+ * device memory (code under HIP graph capture, serving loops, harnesses that
+ * forbid allocation).  Its scratch (rank[T*k] and counts[ceil(T/64)][E+1])
+ * is a fixed array inside the library, one copy per GPU, held until the
+ * process ends; hrm_moe_router_dispatch_noalloc_max_bytes() gives its size,
+ * 1.25 MiB: enough for 32768 tokens at E <= 128 and k <= 8.  A call whose
+ * scratch need (hrm_moe_router_dispatch_workspace_size) exceeds it returns
+ * HRM_MOE_ERR_UNSUPPORTED.  The call allocates nothing and needs nothing
+ * zeroed; every call on one GPU shares that GPU's array, so calls that
+ * overlap on one GPU (other streams, other threads) race: order them on one
+ * stream.
+ */
+size_t hrm_moe_router_dispatch_noalloc_max_bytes(void);
+int hrm_moe_router_topk_dispatch_noalloc(const void* logits, int logits_dtype, int64_t num_tokens,
+                                         int32_t num_experts, int32_t top_k, int32_t norm_topk_prob, float* probs,
+                                         int64_t* topk_idx, void* topk_weight, int weight_dtype,
+                                         int64_t* tokens_per_expert, int32_t* expert_offsets,
+                                         int32_t* sorted_token_idx, int64_t* sort_idx, int32_t* slot_to_row,
+                                         void* stream);
+
+/*
  * Grouped GEMMs over expert-contiguous row groups: rows
  * [sum(tpe[:e]), sum(tpe[:e+1])) belong to expert e.  tokens_per_expert is
  * int64 on the device and is never read on the host.  fp32 accumulation,
