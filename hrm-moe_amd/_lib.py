@@ -45,6 +45,7 @@ PROTOTYPES = {
     "hrm_moe_permute_workspace_size": (_SZ, [_I64, _I32, _I32]),
     "hrm_moe_permute": (_INT, [_P, _I64, _I32, _I32, _P, _P, _P, _P, _P, _P, _SZ, _P]),
     "hrm_moe_grouped_gemm_workspace_size": (_SZ, [_I64, _I32]),
+    "hrm_moe_grouped_wgrad_workspace_size": (_SZ, [_I64, _I64, _I64, _I32]),
     "hrm_moe_grouped_gemm_nt": (_INT, [_P, _P, _P, _I64, _I64, _I64, _I32, _INT, _P, _P, _SZ, _P]),
     "hrm_moe_grouped_gemm_nn": (_INT, [_P, _P, _P, _I64, _I64, _I64, _I32, _INT, _P, _P, _SZ, _P]),
     "hrm_moe_grouped_gemm_tn": (_INT, [_P, _P, _P, _I64, _I64, _I64, _I32, _INT, _P, _P, _SZ, _P]),

@@ -537,6 +537,224 @@ __global__ __launch_bounds__(256) void sum_splits_kernel(const float* __restrict
 }
 
 // ---------------------------------------------------------------------------
+// Wgrad work plan: row groups, split and balanced by cost
+// ---------------------------------------------------------------------------
+// A wgrad work item is one output tile of one group of rows.  A group is an
+// expert's rows or, for an expert holding more than `chunk` rows, one chunk
+// of at most `chunk` consecutive rows of it.  The groups of a chunked expert
+// accumulate into fp32 partial slots that wgrad_finish_kernel adds in chunk
+// order and rounds once, so results are deterministic and independent of
+// the grid.  An item's cost is about its group's row count, so the plan:
+//   * cuts the group list (expert order) into 8 contiguous runs of about
+//     equal total rows, one per XCD, so each expert's rows stay in one L2;
+//   * orders each run by rows, largest first, so the longest items start
+//     first and the XCD's workgroups finish together.
+// (The reference's K-grouped kernel walks an expert's whole row range for
+// every output tile, models/moe_triton_grouped_gemm.py:341-345, so one
+// heavily loaded expert bounds its time.)
+struct WGroup {
+  int32_t expert, row_start, row_end, slot;  // slot: fp32 partial slot, or -1 to store C[expert] directly
+};
+constexpr int kChunkMin = 2048;  // smallest chunk: near-uniform loads (2 x the mean at most) are never split
+
+inline int wgrad_gmax(int E) { return E + E / 2 + 2; }  // groups: E + M / chunk with chunk >= 2 M / E
+inline size_t wgrad_plan_bytes(int E) {
+  const int g = wgrad_gmax(E);
+  return align256(sizeof(int) * (E + 1)) + align256(sizeof(WGroup) * g) + align256(sizeof(int) * g) +
+         align256(sizeof(int) * 64) + align256(sizeof(int4) * E);
+}
+// chunk rows of a plan with partial slots: 2 x the mean rows per expert, at least kChunkMin
+inline int64_t wgrad_chunk(int64_t M, int E) {
+  const int64_t c = 2 * ((M + E - 1) / E);
+  return c < kChunkMin ? kChunkMin : c;
+}
+// partial slots the first chunk size can need: chunked experts hold more than
+// `chunk` rows each, so their chunks number less than 2 M / chunk (and E)
+inline int wgrad_slots_needed(int64_t M, int E) {
+  const int64_t s = 2 * M / wgrad_chunk(M, E);
+  return (int)(s < E ? s : E);
+}
+
+struct WgradPlan {
+  int* row_offsets;  // [E + 1]
+  WGroup* groups;    // [gmax]
+  int* order;        // [gmax]: group ids, the 8 XCD runs one after another, each largest first
+  int* info;         // [64]: run start and count per XCD [0, 16), group count [16], split count [17],
+                     //       work counters [32, 40)
+  int4* splits;      // [E]: chunked expert, first slot, chunks
+  float* partials;   // [max_slots][Na * Nb]
+  int max_slots;
+};
+
+inline WgradPlan carve_wgrad(void* ws, size_t ws_bytes, int E, int64_t na_nb) {
+  char* p = static_cast<char*>(ws);
+  const int g = wgrad_gmax(E);
+  WgradPlan w;
+  w.row_offsets = reinterpret_cast<int*>(p);
+  p += align256(sizeof(int) * (E + 1));
+  w.groups = reinterpret_cast<WGroup*>(p);
+  p += align256(sizeof(WGroup) * g);
+  w.order = reinterpret_cast<int*>(p);
+  p += align256(sizeof(int) * g);
+  w.info = reinterpret_cast<int*>(p);
+  p += align256(sizeof(int) * 64);
+  w.splits = reinterpret_cast<int4*>(p);
+  p += align256(sizeof(int4) * E);
+  w.partials = reinterpret_cast<float*>(p);
+  const size_t used = wgrad_plan_bytes(E);
+  const size_t slot_bytes = sizeof(float) * (size_t)na_nb;
+  size_t slots = ws_bytes > used && slot_bytes ? (ws_bytes - used) / slot_bytes : 0;
+  w.max_slots = (int)(slots > (size_t)E ? (size_t)E : slots);
+  return w;
+}
+
+// Inclusive scan of v[0, n) in LDS, n <= 2048, by a 1024-thread block.
+__device__ void block_scan_i64(int64_t* v, int n) {
+  for (int off = 1; off < n; off <<= 1) {
+    int64_t a = 0, b = 0;
+    const int i0 = threadIdx.x, i1 = threadIdx.x + 1024;
+    if (i0 < n && i0 >= off) a = v[i0 - off];
+    if (i1 < n && i1 >= off) b = v[i1 - off];
+    __syncthreads();
+    if (i0 < n && i0 >= off) v[i0] += a;
+    if (i1 < n && i1 >= off) v[i1] += b;
+    __syncthreads();
+  }
+}
+
+// One block of 1024 threads; E <= 1024.  max_slots = 0 keeps every expert whole.
+__global__ __launch_bounds__(1024) void wgrad_plan_kernel(const int64_t* __restrict__ tpe, int E, int64_t M,
+                                                          int64_t chunk0, WgradPlan w) {
+  __shared__ int64_t s_a[2048];  // scans (per expert, then per group)
+  __shared__ uint64_t s_key[2048];
+  __shared__ int s_rs[1024], s_n[1024], s_c[1024], s_gb[1024], s_sb[1024];
+  __shared__ int64_t s_chunk;
+  __shared__ int s_need;
+  const int tid = threadIdx.x;
+  // expert row ranges: prefix of the counts, clamped to M
+  for (int e = tid; e < 1024; e += 1024) s_a[e] = e < E && tpe[e] > 0 ? tpe[e] : 0;
+  __syncthreads();
+  block_scan_i64(s_a, E);
+  if (tid < E) {
+    const int64_t end = s_a[tid], start = tid == 0 ? 0 : s_a[tid - 1];
+    const int rs = (int)(start < M ? start : M), re = (int)(end < M ? end : M);
+    s_rs[tid] = rs;
+    s_n[tid] = re - rs;
+    w.row_offsets[tid] = rs;
+    if (tid == E - 1) w.row_offsets[E] = re;
+  }
+  if (tid == 0) s_chunk = w.max_slots > 0 ? chunk0 : ((int64_t)1 << 40);
+  __syncthreads();
+  // chunk size: the smallest power-of-two multiple of chunk0 whose chunks fit the partial slots
+  while (true) {
+    if (tid == 0) s_need = 0;
+    __syncthreads();
+    const int64_t ch = s_chunk;
+    if (tid < E && s_n[tid] > ch) atomicAdd(&s_need, (int)((s_n[tid] + ch - 1) / ch));
+    __syncthreads();
+    const bool fits = s_need <= w.max_slots;
+    __syncthreads();
+    if (fits) break;
+    if (tid == 0) s_chunk = ch * 2;
+    __syncthreads();
+  }
+  const int64_t ch = s_chunk;
+  // groups and partial slots per expert: exclusive prefixes
+  if (tid < E) s_c[tid] = s_n[tid] > ch ? (int)((s_n[tid] + ch - 1) / ch) : 1;
+  for (int e = tid; e < 1024; e += 1024) s_a[e] = e < E ? s_c[e] : 0;
+  __syncthreads();
+  block_scan_i64(s_a, E);
+  if (tid < E) s_gb[tid] = (int)(s_a[tid] - s_c[tid]);
+  const int G = (int)s_a[E - 1];
+  __syncthreads();
+  for (int e = tid; e < 1024; e += 1024) s_a[e] = e < E && s_c[e] > 1 ? s_c[e] : 0;
+  __syncthreads();
+  block_scan_i64(s_a, E);
+  if (tid < E) s_sb[tid] = (int)(s_a[tid] - (s_c[tid] > 1 ? s_c[tid] : 0));
+  __syncthreads();
+  for (int e = tid; e < 1024; e += 1024) s_a[e] = e < E && s_c[e] > 1 ? 1 : 0;
+  __syncthreads();
+  block_scan_i64(s_a, E);
+  if (tid < E && s_c[tid] > 1) w.splits[s_a[tid] - 1] = int4{tid, s_sb[tid], s_c[tid], 0};
+  const int nsplit = (int)s_a[E - 1];
+  __syncthreads();
+  // the groups, their costs and their prefix
+  for (int g = tid; g < 2048; g += 1024) {
+    int64_t cost = 0;
+    if (g < G) {
+      int lo = 0, hi = E - 1;  // expert of group g: the last e with s_gb[e] <= g
+      while (lo < hi) {
+        const int mid = (lo + hi + 1) >> 1;
+        if (s_gb[mid] <= g) lo = mid; else hi = mid - 1;
+      }
+      const int e = lo, c = g - s_gb[e];
+      WGroup grp;
+      grp.expert = e;
+      grp.row_start = s_rs[e] + (int)(c * ch);
+      const int64_t end = (int64_t)grp.row_start + ch;
+      grp.row_end = (int)(end < s_rs[e] + s_n[e] ? end : s_rs[e] + s_n[e]);
+      grp.slot = s_c[e] > 1 ? s_sb[e] + c : -1;
+      w.groups[g] = grp;
+      cost = (int64_t)(grp.row_end - grp.row_start) + 64;  // + a tile's fixed cost, so empty groups count
+    }
+    s_a[g] = cost;
+  }
+  __syncthreads();
+  block_scan_i64(s_a, G);
+  const int64_t total = s_a[G - 1];
+  // XCD of a group: where its cost's midpoint falls in eighths of the total; then
+  // sort by (XCD, cost descending, group id)
+  for (int g = tid; g < 2048; g += 1024) {
+    uint64_t key = ~0ull;
+    if (g < G) {
+      const int64_t cost = g == 0 ? s_a[0] : s_a[g] - s_a[g - 1];
+      int64_t x = ((s_a[g] - cost / 2) * 8) / total;
+      x = x < 7 ? x : 7;
+      key = ((uint64_t)x << 56) | ((uint64_t)(0xFFFFFFFFu - (uint32_t)cost) << 16) | (uint64_t)g;
+    }
+    s_key[g] = key;
+  }
+  __syncthreads();
+  int P = 1;
+  while (P < G) P <<= 1;
+  for (int k = 2; k <= P; k <<= 1) {
+    for (int j = k >> 1; j > 0; j >>= 1) {
+      for (int i = tid; i < P; i += 1024) {
+        const int l = i ^ j;
+        if (l > i) {
+          const uint64_t a = s_key[i], b = s_key[l];
+          const bool up = (i & k) == 0;
+          if ((a > b) == up) {
+            s_key[i] = b;
+            s_key[l] = a;
+          }
+        }
+      }
+      __syncthreads();
+    }
+  }
+  if (tid < 16) w.info[tid] = 0;
+  if (tid >= 32 && tid < 40) w.info[tid] = 0;  // work counters
+  __syncthreads();
+  for (int i = tid; i < G; i += 1024) {
+    const uint64_t key = s_key[i];
+    const int x = (int)(key >> 56);
+    w.order[i] = (int)(key & 0xFFFF);
+    if (i == 0 || (int)(s_key[i - 1] >> 56) != x) w.info[2 * x] = i;
+    if (i == G - 1 || (int)(s_key[i + 1] >> 56) != x) w.info[2 * x + 1] = i + 1;  // end, made a count below
+  }
+  __syncthreads();
+  if (tid < 8) {
+    const int end = w.info[2 * tid + 1];
+    w.info[2 * tid + 1] = end > 0 ? end - w.info[2 * tid] : 0;
+  }
+  if (tid == 0) {
+    w.info[16] = G;
+    w.info[17] = nsplit;
+  }
+}
+
+// ---------------------------------------------------------------------------
 // DMA-fed kernels: buffer_load ... lds fills a ring of LDS stages directly
 // ---------------------------------------------------------------------------
 // Each buffer_load_dwordx4 ... lds writes the 16 bytes of lane L to
@@ -1288,11 +1506,13 @@ __global__ __launch_bounds__(256) void mgemm_skinny_kernel(const uint16_t* __res
 }
 
 // Wgrad with 8 waves on BA x BB = 256 x 256 tiles of C[e] (128 x 64 per
-// wave), both operands DMA-fed as [64 k][cols] slices of the expert's rows
-// and read transposed.  Tiles are handed out by one atomic counter per XCD
-// over that XCD's contiguous eighth of the (expert, na-tile, nb-tile) list,
-// so an expert's rows stay in few L2s and ragged experts still balance.  The
-// epilogue is staged through the idle ring like the M-grouped kernels'.
+// wave), both operands DMA-fed as [64 k][cols] slices of a row group and
+// read transposed.  Work items are (row group, na-tile, nb-tile), taken
+// with one atomic counter per XCD from that XCD's run of the wgrad plan
+// (wgrad_plan_kernel: runs of about equal rows, largest groups first), so
+// an expert's rows stay in one L2 and skewed loads still balance.  The
+// epilogue of a whole expert is staged through the idle ring like the
+// M-grouped kernels'; a chunk of a split expert stores fp32 partial sums.
 // GB: the B operand's rows are gathered, B[b_index[row]] (B is [b_rows, Nb]),
 // as the gate_up wgrad reads the hidden rows of the expert's tokens.  Each lane
 // keeps the source rows of its k rows for the next step to be issued, loaded
@@ -1301,10 +1521,8 @@ __global__ __launch_bounds__(256) void mgemm_skinny_kernel(const uint16_t* __res
 template <typename TR, int BA, int BB, int NW, int STAGES, bool GB = false>
 __global__ __launch_bounds__(NW * 64, 1) void wgrad_dma8_kernel(const uint16_t* __restrict__ A,
                                                                 const uint16_t* __restrict__ B,
-                                                                uint16_t* __restrict__ C,
-                                                                const int* __restrict__ row_offsets, int E, int Na,
-                                                                int Nb, int* __restrict__ counters,
-                                                                const int32_t* __restrict__ b_index,
+                                                                uint16_t* __restrict__ C, WgradPlan plan, int Na,
+                                                                int Nb, const int32_t* __restrict__ b_index,
                                                                 uint32_t b_bytes) {
   static_assert(!GB || STAGES == 2, "gathered B needs the 2-stage ring (its issue waits for every load)");
   constexpr int WGN = NW / 2;
@@ -1327,22 +1545,21 @@ __global__ __launch_bounds__(NW * 64, 1) void wgrad_dma8_kernel(const uint16_t* 
   const int wm = wave / WGN, wn = wave % WGN;
   const int ta_n = (Na + BA - 1) / BA, tb_n = (Nb + BB - 1) / BB;
   const int per_e = ta_n * tb_n;
-  const int total = E * per_e;
   const int xcd = blockIdx.x & 7;
-  const int chunk = (total + 7) >> 3;
-  const int t_begin = xcd * chunk;
-  const int t_end = min(total, t_begin + chunk);
+  const int run0 = plan.info[2 * xcd];
+  const int items = plan.info[2 * xcd + 1] * per_e;
 
   while (true) {
-    if (tid == 0) s_tile = t_begin + atomicAdd(&counters[xcd], 1);
+    if (tid == 0) s_tile = atomicAdd(&plan.info[32 + xcd], 1);
     __syncthreads();  // also orders the previous tile's staging reads before this tile's DMA
     const int t = s_tile;
     __syncthreads();
-    if (t >= t_end) break;
-    const int e = t / per_e;
-    const int rem = t - e * per_e;
+    if (t >= items) break;
+    const WGroup grp = plan.groups[plan.order[run0 + t / per_e]];
+    const int rem = t % per_e;
     const int a0 = (rem / tb_n) * BA, b0 = (rem % tb_n) * BB;
-    const int rs = row_offsets[e], re = row_offsets[e + 1];
+    const int e = grp.expert, rs = grp.row_start, re = grp.row_end;
+    const int slot = __builtin_amdgcn_readfirstlane(grp.slot);
     const int nk = (re - rs + kBK - 1) / kBK;
     const __amdgpu_buffer_rsrc_t rA = make_rsrc(A + (int64_t)rs * Na, (uint32_t)(re - rs) * (uint32_t)Na * 2);
     const __amdgpu_buffer_rsrc_t rB =
@@ -1428,7 +1645,23 @@ __global__ __launch_bounds__(NW * 64, 1) void wgrad_dma8_kernel(const uint16_t* 
 
     // Epilogue: no DMA is in flight (every issued step was consumed), so once
     // all waves pass the barrier the whole ring is free for staging.
-    {
+    if (slot >= 0) {
+      // a chunk of a split expert: fp32 partial sums straight from the accumulators
+      float* P = plan.partials + (int64_t)slot * Na * Nb;
+#pragma unroll
+      for (int a = 0; a < MB; ++a) {
+        const int na = a0 + wm * (BA / 2) + a * 32 + (lane & 31);
+#pragma unroll
+        for (int b = 0; b < NB; ++b)
+#pragma unroll
+          for (int gq = 0; gq < 4; ++gq) {
+            const int nb = b0 + wn * (BB / WGN) + b * 32 + gq * 8 + (lane >> 5) * 4;
+            if (na < Na && nb < Nb)
+              *reinterpret_cast<floatx4*>(P + (int64_t)na * Nb + nb) =
+                  floatx4{acc[b][a][gq * 4 + 0], acc[b][a][gq * 4 + 1], acc[b][a][gq * 4 + 2], acc[b][a][gq * 4 + 3]};
+          }
+      }
+    } else {
       constexpr int WCOLS = BB / WGN;                     // output columns (nb) per wave
       constexpr int PITCH = WCOLS * 2;
       constexpr int C8 = PITCH / 8;
@@ -1478,17 +1711,17 @@ __global__ __launch_bounds__(NW * 64, 1) void wgrad_dma8_kernel(const uint16_t* 
   wait_vmcnt<0>();
 }
 
-// Wgrad fed by DMA: both operands are [64 rows][128 cols] tiles of the
-// expert's rows; rows past the expert's end read as zeros (buffer bounds).
+// Wgrad fed by DMA: both operands are [64 rows][128 cols] tiles of a row
+// group; rows past the group's end read as zeros (buffer bounds).  Work
+// items (group, na-tile, nb-tile) come from one atomic counter over all
+// groups of the wgrad plan in its order.
 // GB: gathered B rows, as in wgrad_dma8_kernel.  F32OUT: C is fp32 (the
 // per-split partial sums of the router gate's weight gradient).
 template <typename TR, int STAGES, bool GB = false, bool F32OUT = false>
 __global__ __launch_bounds__(kThreads, 1) void wgrad_dma_kernel(const uint16_t* __restrict__ A,
                                                                const uint16_t* __restrict__ B,
-                                                               uint16_t* __restrict__ C,
-                                                               const int* __restrict__ row_offsets, int E, int Na,
-                                                               int Nb, int* __restrict__ work_counter,
-                                                               const int32_t* __restrict__ b_index,
+                                                               uint16_t* __restrict__ C, WgradPlan plan, int Na,
+                                                               int Nb, const int32_t* __restrict__ b_index,
                                                                uint32_t b_bytes) {
   static_assert(!GB || STAGES == 2, "gathered B needs the 2-stage ring (its issue waits for every load)");
   constexpr int BA = 128, BB = 128;
@@ -1503,18 +1736,19 @@ __global__ __launch_bounds__(kThreads, 1) void wgrad_dma_kernel(const uint16_t* 
   const int wa = wave >> 1, wb = wave & 1;
   const int ta_n = (Na + BA - 1) / BA, tb_n = (Nb + BB - 1) / BB;
   const int per_e = ta_n * tb_n;
-  const int total = E * per_e;
+  const int total = plan.info[16] * per_e;
 
   while (true) {
-    if (tid == 0) s_tile = atomicAdd(work_counter, 1);
+    if (tid == 0) s_tile = atomicAdd(&plan.info[32], 1);
     __syncthreads();
     const int t = s_tile;
     __syncthreads();
     if (t >= total) break;
-    const int e = t / per_e;
-    const int rem = t - e * per_e;
+    const WGroup grp = plan.groups[plan.order[t / per_e]];
+    const int rem = t % per_e;
     const int a0 = (rem / tb_n) * BA, b0 = (rem % tb_n) * BB;
-    const int rs = row_offsets[e], re = row_offsets[e + 1];
+    const int e = grp.expert, rs = grp.row_start, re = grp.row_end;
+    const int slot = __builtin_amdgcn_readfirstlane(grp.slot);
     const int nk = (re - rs + kBK - 1) / kBK;
     const __amdgpu_buffer_rsrc_t rA = make_rsrc(A + (int64_t)rs * Na, (uint32_t)(re - rs) * (uint32_t)Na * 2);
     const __amdgpu_buffer_rsrc_t rB =
@@ -1593,7 +1827,8 @@ __global__ __launch_bounds__(kThreads, 1) void wgrad_dma_kernel(const uint16_t* 
     barrier_lds();
 
     uint16_t* Ce = C + (int64_t)e * Na * Nb;
-    float* Cf = reinterpret_cast<float*>(C) + (int64_t)e * Na * Nb;
+    // fp32 destination: a split expert's partial slot, or C itself for F32OUT
+    float* Cf = slot >= 0 ? plan.partials + (int64_t)slot * Na * Nb : reinterpret_cast<float*>(C) + (int64_t)e * Na * Nb;
 #pragma unroll
     for (int a = 0; a < MB; ++a) {
       const int na = a0 + wa * (BA / 2) + a * 32 + (lane & 31);
@@ -1604,7 +1839,7 @@ __global__ __launch_bounds__(kThreads, 1) void wgrad_dma_kernel(const uint16_t* 
         for (int g = 0; g < 4; ++g) {
           const int nb = b0 + wb * (BB / 2) + b * 32 + g * 8 + (lane >> 5) * 4;
           if (nb >= Nb) continue;
-          if constexpr (F32OUT)
+          if (F32OUT || slot >= 0)
             *reinterpret_cast<floatx4*>(Cf + (int64_t)na * Nb + nb) =
                 floatx4{acc[b][a][g * 4 + 0], acc[b][a][g * 4 + 1], acc[b][a][g * 4 + 2], acc[b][a][g * 4 + 3]};
           else
@@ -1652,7 +1887,10 @@ int check_common(int64_t M, int32_t E, int dtype, const void* ws, size_t ws_byte
   if (M < 0 || E < 1) return HRM_MOE_ERR_INVALID;
   if (dtype != HRM_MOE_BF16 && dtype != HRM_MOE_F16) return HRM_MOE_ERR_DTYPE;
   if (E > kMaxExperts || M >= (int64_t(1) << 31)) return HRM_MOE_ERR_UNSUPPORTED;
-  if (!ws || ws_bytes < gemm_ws_bytes(M, E, kBMMin)) return HRM_MOE_ERR_WORKSPACE;
+  // the size hrm_moe_grouped_gemm_workspace_size reports: the M-tile plan or the wgrad plan
+  const size_t need = gemm_ws_bytes(M, E, kBMMin) > wgrad_plan_bytes(E) ? gemm_ws_bytes(M, E, kBMMin)
+                                                                         : wgrad_plan_bytes(E);
+  if (!ws || ws_bytes < need) return HRM_MOE_ERR_WORKSPACE;
   return HRM_MOE_OK;
 }
 
@@ -1855,19 +2093,51 @@ int dispatch_mgemm(int dtype, const void* A, const int32_t* gather, const void* 
   return dispatch_mgemm_t<F16, KIND>(A, gather, W, tpe, M, N, K, E, a_rows, C, workspace, stream);
 }
 
+// Adds each split expert's partial slots in chunk order and rounds once into
+// C[e]; a grid-stride loop over (split expert, 4 elements), so a plan without
+// splits costs one short launch.
+template <typename TR>
+__global__ __launch_bounds__(256) void wgrad_finish_kernel(const float* __restrict__ partials,
+                                                           const int4* __restrict__ splits,
+                                                           const int* __restrict__ info, int64_t n,
+                                                           uint16_t* __restrict__ C) {
+  const int64_t quads = n / 4;
+  const int64_t total = (int64_t)info[17] * quads;
+  for (int64_t q = (int64_t)blockIdx.x * 256 + threadIdx.x; q < total; q += (int64_t)gridDim.x * 256) {
+    const int64_t si = q / quads;
+    const int64_t i = (q - si * quads) * 4;
+    const int4 sp = splits[si];
+    floatx4 acc = floatx4{0.f, 0.f, 0.f, 0.f};
+    for (int c = 0; c < sp.z; ++c) acc += *reinterpret_cast<const floatx4*>(partials + (int64_t)(sp.y + c) * n + i);
+    st8(C + (int64_t)sp.x * n + i, pack4<TR>(acc[0], acc[1], acc[2], acc[3]));
+  }
+}
+
+// Workspace of the wgrad entry points: the tile plan of the register-staged
+// fallback or the wgrad plan, whichever is larger; with room for partial slots
+// beyond it, heavily loaded experts are split (hrm_moe_grouped_wgrad_workspace_size).
+inline size_t wgrad_base_bytes(int64_t M, int E) {
+  const size_t a = gemm_ws_bytes(M, E, kBMMin), b = wgrad_plan_bytes(E);
+  return a > b ? a : b;
+}
+inline size_t wgrad_full_bytes(int64_t M, int E, int64_t Na, int64_t Nb) {
+  return wgrad_base_bytes(M, E) + align256(sizeof(float) * (size_t)wgrad_slots_needed(M, E) * (size_t)(Na * Nb));
+}
+
 template <typename TR>
 int launch_wgrad(const void* A, const void* B, const int64_t* tpe, int64_t M, int Na, int Nb, int E, void* C,
-                 void* workspace, void* stream, const int32_t* b_index = nullptr, int64_t b_rows = 0) {
-  GemmWs w = carve(workspace, M, E, kBMMin);
-  const int max_tiles = (int)((M + kBMMin - 1) / kBMMin + E);
-  HRM_LAUNCH(plan_kernel, dim3(1), dim3(1024), 0, stream, tpe, E, M, kBMMin, w.tiles, max_tiles, w.count,
-             w.row_offsets, w.work_counter);
+                 void* workspace, size_t ws_bytes, void* stream, const int32_t* b_index = nullptr,
+                 int64_t b_rows = 0) {
   const bool gather = b_index != nullptr;
   const int64_t b_span = gather ? b_rows : M;
   const bool dma = M * (int64_t)Na * 2 < (int64_t(1) << 32) && b_span * (int64_t)Nb * 2 < (int64_t(1) << 32);
   const uint32_t b_bytes = (uint32_t)(b_span * (int64_t)Nb * 2);
   if (!dma) {
     if (gather) return HRM_MOE_ERR_UNSUPPORTED;  // operands beyond 32-bit buffer offsets
+    GemmWs w = carve(workspace, M, E, kBMMin);
+    const int max_tiles = (int)((M + kBMMin - 1) / kBMMin + E);
+    HRM_LAUNCH(plan_kernel, dim3(1), dim3(1024), 0, stream, tpe, E, M, kBMMin, w.tiles, max_tiles, w.count,
+               w.row_offsets, w.work_counter);
     auto kern = wgrad_kernel<TR, 128, 128>;
     static GridCache gc;
     const int grid = gc.get(kern);
@@ -1875,6 +2145,10 @@ int launch_wgrad(const void* A, const void* B, const int64_t* tpe, int64_t M, in
                w.row_offsets, E, Na, Nb, w.work_counter);
     return HRM_MOE_OK;
   }
+  // the plan sits after the fallback's tile plan region, so both fit the base size
+  const size_t skip = align256(wgrad_base_bytes(M, E) - wgrad_plan_bytes(E));
+  WgradPlan plan = carve_wgrad(static_cast<char*>(workspace) + skip, ws_bytes - skip, E, (int64_t)Na * Nb);
+  HRM_LAUNCH(wgrad_plan_kernel, dim3(1), dim3(1024), 0, stream, tpe, E, M, wgrad_chunk(M, E), plan);
   // 256 x 256 tiles with 8 waves when both widths fill them and experts have
   // enough rows to amortise a tile; HRM_MOE_WGRAD_STAGES=2|3 selects the
   // 128 x 128 four-wave kernel instead (gathered B: 2 stages).
@@ -1884,36 +2158,42 @@ int launch_wgrad(const void* A, const void* B, const int64_t* tpe, int64_t M, in
       auto kern = wgrad_dma8_kernel<TR, 256, 256, 8, 2, true>;
       static GridCache gc;
       const int grid = gc.get(kern, 512);
-      HRM_LAUNCH(kern, dim3(grid), dim3(512), 0, stream, (const uint16_t*)A, (const uint16_t*)B, (uint16_t*)C,
-                 w.row_offsets, E, Na, Nb, w.work_counter, b_index, b_bytes);
+      HRM_LAUNCH(kern, dim3(grid), dim3(512), 0, stream, (const uint16_t*)A, (const uint16_t*)B, (uint16_t*)C, plan,
+                 Na, Nb, b_index, b_bytes);
     } else {
       auto kern = wgrad_dma8_kernel<TR, 256, 256, 8, 2>;
       static GridCache gc;
       const int grid = gc.get(kern, 512);
-      HRM_LAUNCH(kern, dim3(grid), dim3(512), 0, stream, (const uint16_t*)A, (const uint16_t*)B, (uint16_t*)C,
-                 w.row_offsets, E, Na, Nb, w.work_counter, nullptr, 0u);
+      HRM_LAUNCH(kern, dim3(grid), dim3(512), 0, stream, (const uint16_t*)A, (const uint16_t*)B, (uint16_t*)C, plan,
+                 Na, Nb, nullptr, 0u);
     }
-    return HRM_MOE_OK;
-  }
-  const int stages = gather || wstages == 2 ? 2 : 3;
-  if (gather) {
-    auto kern = wgrad_dma_kernel<TR, 2, true>;
-    static GridCache gc;
-    const int grid = gc.get(kern);
-    HRM_LAUNCH(kern, dim3(grid), dim3(kThreads), 0, stream, (const uint16_t*)A, (const uint16_t*)B, (uint16_t*)C,
-               w.row_offsets, E, Na, Nb, w.work_counter, b_index, b_bytes);
-  } else if (stages == 2) {
-    auto kern = wgrad_dma_kernel<TR, 2>;
-    static GridCache gc;
-    const int grid = gc.get(kern);
-    HRM_LAUNCH(kern, dim3(grid), dim3(kThreads), 0, stream, (const uint16_t*)A, (const uint16_t*)B, (uint16_t*)C,
-               w.row_offsets, E, Na, Nb, w.work_counter, nullptr, 0u);
   } else {
-    auto kern = wgrad_dma_kernel<TR, 3>;
-    static GridCache gc;
-    const int grid = gc.get(kern);
-    HRM_LAUNCH(kern, dim3(grid), dim3(kThreads), 0, stream, (const uint16_t*)A, (const uint16_t*)B, (uint16_t*)C,
-               w.row_offsets, E, Na, Nb, w.work_counter, nullptr, 0u);
+    const int stages = gather || wstages == 2 ? 2 : 3;
+    if (gather) {
+      auto kern = wgrad_dma_kernel<TR, 2, true>;
+      static GridCache gc;
+      const int grid = gc.get(kern);
+      HRM_LAUNCH(kern, dim3(grid), dim3(kThreads), 0, stream, (const uint16_t*)A, (const uint16_t*)B, (uint16_t*)C,
+                 plan, Na, Nb, b_index, b_bytes);
+    } else if (stages == 2) {
+      auto kern = wgrad_dma_kernel<TR, 2>;
+      static GridCache gc;
+      const int grid = gc.get(kern);
+      HRM_LAUNCH(kern, dim3(grid), dim3(kThreads), 0, stream, (const uint16_t*)A, (const uint16_t*)B, (uint16_t*)C,
+                 plan, Na, Nb, nullptr, 0u);
+    } else {
+      auto kern = wgrad_dma_kernel<TR, 3>;
+      static GridCache gc;
+      const int grid = gc.get(kern);
+      HRM_LAUNCH(kern, dim3(grid), dim3(kThreads), 0, stream, (const uint16_t*)A, (const uint16_t*)B, (uint16_t*)C,
+                 plan, Na, Nb, nullptr, 0u);
+    }
+  }
+  if (plan.max_slots >= 2) {
+    const int64_t n = (int64_t)Na * Nb;
+    const int64_t blocks = (n / 4 * (plan.max_slots / 2) + 255) / 256;
+    HRM_LAUNCH(wgrad_finish_kernel<TR>, dim3((unsigned)(blocks < 2048 ? blocks : 2048)), dim3(256), 0, stream,
+               plan.partials, plan.splits, plan.info, n, (uint16_t*)C);
   }
   return HRM_MOE_OK;
 }
@@ -1931,7 +2211,7 @@ inline int gate_wgrad_splits(int64_t T) {
 }
 inline size_t gate_wgrad_ws_bytes(int64_t T, int E, int64_t H) {
   const int S = gate_wgrad_splits(T);
-  return align256(sizeof(int64_t) * S) + align256(gemm_ws_bytes(T, S, kBMMin)) + align256(sizeof(float) * S * E * H);
+  return align256(sizeof(int64_t) * S) + align256(wgrad_plan_bytes(S)) + align256(sizeof(float) * S * E * H);
 }
 
 template <typename TR>
@@ -1941,19 +2221,17 @@ int launch_gate_wgrad(const void* dlogits, const void* hidden, int64_t T, int E,
   char* p = static_cast<char*>(ws);
   int64_t* tpe = reinterpret_cast<int64_t*>(p);
   p += align256(sizeof(int64_t) * S);
-  void* gws = p;
-  p += align256(gemm_ws_bytes(T, S, kBMMin));
+  // the splits are the groups of a plan without partial slots
+  const WgradPlan plan = carve_wgrad(p, wgrad_plan_bytes(S), S, (int64_t)E * H);
+  p += align256(wgrad_plan_bytes(S));
   float* part = reinterpret_cast<float*>(p);
   HRM_LAUNCH(split_rows_kernel, dim3((S + 255) / 256), dim3(256), 0, stream, tpe, S, T);
-  GemmWs w = carve(gws, T, S, kBMMin);
-  const int max_tiles = (int)((T + kBMMin - 1) / kBMMin + S);
-  HRM_LAUNCH(plan_kernel, dim3(1), dim3(1024), 0, stream, tpe, S, T, kBMMin, w.tiles, max_tiles, w.count,
-             w.row_offsets, w.work_counter);
+  HRM_LAUNCH(wgrad_plan_kernel, dim3(1), dim3(1024), 0, stream, tpe, S, T, (int64_t)T, plan);
   auto kern = wgrad_dma_kernel<TR, 2, false, true>;
   static GridCache gc;
   const int grid = gc.get(kern);
   HRM_LAUNCH(kern, dim3(grid), dim3(kThreads), 0, stream, (const uint16_t*)dlogits, (const uint16_t*)hidden,
-             (uint16_t*)part, w.row_offsets, S, E, H, w.work_counter, nullptr, 0u);
+             (uint16_t*)part, plan, E, H, nullptr, 0u);
   const int64_t n = (int64_t)E * H;
   HRM_LAUNCH(sum_splits_kernel<TR>, dim3((unsigned)((n / 4 + 255) / 256)), dim3(256), 0, stream, part, S, n,
              (uint16_t*)out);
@@ -1995,7 +2273,13 @@ extern "C" int hrm_moe_gate_wgrad(const void* grad_logits, const void* hidden, i
 
 extern "C" size_t hrm_moe_grouped_gemm_workspace_size(int64_t num_rows, int32_t num_experts) {
   if (num_rows < 0 || num_experts < 1 || num_experts > hrm::kMaxExperts) return 0;
-  return hrm::gemm_ws_bytes(num_rows, num_experts, hrm::kBMMin);
+  return hrm::wgrad_base_bytes(num_rows, num_experts);
+}
+
+extern "C" size_t hrm_moe_grouped_wgrad_workspace_size(int64_t num_rows, int64_t Na, int64_t Nb,
+                                                       int32_t num_experts) {
+  if (num_rows < 0 || num_experts < 1 || num_experts > hrm::kMaxExperts || Na < 1 || Nb < 1) return 0;
+  return hrm::wgrad_full_bytes(num_rows, num_experts, Na, Nb);
 }
 
 extern "C" int hrm_moe_grouped_gemm_nt(const void* A, const void* W, const int64_t* tokens_per_expert, int64_t M,
@@ -2032,10 +2316,12 @@ extern "C" int hrm_moe_grouped_gemm_tn(const void* A, const void* B, const int64
   if (Na < 1 || Nb < 1) return HRM_MOE_ERR_INVALID;
   if (Na % 8 || Nb % 8 || Na >= (1 << 30) || Nb >= (1 << 30)) return HRM_MOE_ERR_UNSUPPORTED;
   if (!tokens_per_expert || !C || (M > 0 && (!A || !B))) return HRM_MOE_ERR_INVALID;
+  if (workspace_bytes < hrm::wgrad_base_bytes(M, num_experts)) return HRM_MOE_ERR_WORKSPACE;
   if (dtype == HRM_MOE_BF16)
     return hrm::launch_wgrad<hrm::BF16>(A, B, tokens_per_expert, M, (int)Na, (int)Nb, num_experts, C, workspace,
-                                        stream);
-  return hrm::launch_wgrad<hrm::F16>(A, B, tokens_per_expert, M, (int)Na, (int)Nb, num_experts, C, workspace, stream);
+                                        workspace_bytes, stream);
+  return hrm::launch_wgrad<hrm::F16>(A, B, tokens_per_expert, M, (int)Na, (int)Nb, num_experts, C, workspace,
+                                     workspace_bytes, stream);
 }
 
 extern "C" int hrm_moe_gate_up_swiglu(const void* hidden, const int32_t* sorted_token_idx,
@@ -2100,9 +2386,10 @@ extern "C" int hrm_moe_grouped_gemm_tn_gather(const void* A, const void* B, cons
   if (Na < 1 || Nb < 1 || b_rows < 0) return HRM_MOE_ERR_INVALID;
   if (Na % 8 || Nb % 8 || Na >= (1 << 30) || Nb >= (1 << 30)) return HRM_MOE_ERR_UNSUPPORTED;
   if (!tokens_per_expert || !C || (M > 0 && (!A || !B || !b_row_index || b_rows == 0))) return HRM_MOE_ERR_INVALID;
+  if (workspace_bytes < hrm::wgrad_base_bytes(M, num_experts)) return HRM_MOE_ERR_WORKSPACE;
   if (dtype == HRM_MOE_BF16)
     return hrm::launch_wgrad<hrm::BF16>(A, B, tokens_per_expert, M, (int)Na, (int)Nb, num_experts, C, workspace,
-                                        stream, b_row_index, b_rows);
-  return hrm::launch_wgrad<hrm::F16>(A, B, tokens_per_expert, M, (int)Na, (int)Nb, num_experts, C, workspace, stream,
-                                     b_row_index, b_rows);
+                                        workspace_bytes, stream, b_row_index, b_rows);
+  return hrm::launch_wgrad<hrm::F16>(A, B, tokens_per_expert, M, (int)Na, (int)Nb, num_experts, C, workspace,
+                                     workspace_bytes, stream, b_row_index, b_rows);
 }

@@ -250,7 +250,11 @@ def grouped_gemm_nn(a: torch.Tensor, w: torch.Tensor, tokens_per_expert: torch.T
 
 
 def grouped_gemm_tn(a: torch.Tensor, b: torch.Tensor, tokens_per_expert: torch.Tensor) -> torch.Tensor:
-    """C[e][Na,Nb] = A[rows_e]^T @ B[rows_e] (wgrad); experts without rows get zeros."""
+    """C[e][Na,Nb] = A[rows_e]^T @ B[rows_e] (wgrad); experts without rows get zeros.
+
+    The workspace leaves room for the fp32 partial sums of experts split into
+    row chunks (loads above twice the mean), which keeps skewed loads balanced.
+    """
     dev = _require_cuda(a, b)
     m, na = a.shape
     mb, nb = b.shape
@@ -264,7 +268,7 @@ def grouped_gemm_tn(a: torch.Tensor, b: torch.Tensor, tokens_per_expert: torch.T
     e = tpe.numel()
     c = a.new_empty((e, na, nb))
     lib = _lib.lib()
-    ws = _workspace(lib.hrm_moe_grouped_gemm_workspace_size(m, e), dev)
+    ws = _workspace(lib.hrm_moe_grouped_wgrad_workspace_size(m, na, nb, e), dev)
     with _lib.device_guard(dev):
         st = lib.hrm_moe_grouped_gemm_tn(_lib.ptr(a), _lib.ptr(b), _lib.ptr(tpe), m, na, nb, e, dt, _lib.ptr(c),
                                          _lib.ptr(ws), ws.numel(), _lib.stream_of(dev))
@@ -321,7 +325,7 @@ def grouped_gemm_tn_gather(a: torch.Tensor, b: torch.Tensor, b_row_index: torch.
     e = tpe.numel()
     c = a.new_empty((e, na, nb))
     lib = _lib.lib()
-    ws = _workspace(lib.hrm_moe_grouped_gemm_workspace_size(m, e), dev)
+    ws = _workspace(lib.hrm_moe_grouped_wgrad_workspace_size(m, na, nb, e), dev)
     with _lib.device_guard(dev):
         st = lib.hrm_moe_grouped_gemm_tn_gather(_lib.ptr(a), _lib.ptr(b), _lib.ptr(idx), b_rows, _lib.ptr(tpe), m, na,
                                                 nb, e, dt, _lib.ptr(c), _lib.ptr(ws), ws.numel(), _lib.stream_of(dev))

@@ -185,7 +185,14 @@ int hrm_moe_grouped_gemm_nn(const void* A, const void* W, const int64_t* tokens_
 /* C[e][Na,Nb] = A[rows_e]^T . B[rows_e] with A [M,Na], B [M,Nb] (wgrad); an
  * expert without rows gets zeros.
  * Replaces _k_grouped_gemm (moe_triton_grouped_gemm.py:420-456) and
- * _k_grouped_gemm_kernel (:277-347), called from the backward at :474. */
+ * _k_grouped_gemm_kernel (:277-347), called from the backward at :474.
+ * Workspace: at least hrm_moe_grouped_gemm_workspace_size(M, E).  With
+ * hrm_moe_grouped_wgrad_workspace_size(M, Na, Nb, E) bytes, an expert holding
+ * more than twice the mean rows (and at least 2048) is reduced in row
+ * chunks into fp32 partial sums that are added in chunk order and rounded
+ * once, so skewed loads keep every workgroup busy; results stay
+ * deterministic and independent of the grid size. */
+size_t hrm_moe_grouped_wgrad_workspace_size(int64_t num_rows, int64_t Na, int64_t Nb, int32_t num_experts);
 int hrm_moe_grouped_gemm_tn(const void* A, const void* B, const int64_t* tokens_per_expert, int64_t M,
                             int64_t Na, int64_t Nb, int32_t num_experts, int dtype, void* C, void* workspace,
                             size_t workspace_bytes, void* stream);
