@@ -894,6 +894,15 @@ __global__ __launch_bounds__(NW * 64, NW == 4 ? 2 : 1) void mgemm_dma_kernel(con
   constexpr int B_INSTR = KIND == KIND_NN ? NN_KR / NN_RPI : B_ROWS / RPIK;
   static_assert(BK == 32 || BK == 64, "K step is 32 or 64");
   constexpr int PER = A_INSTR + B_INSTR;                     // loads per wave per stage
+  // 8 waves, 2-stage ring: the second half of the waves issues its share of a
+  // stage after its first sub-step of MFMAs.  Issued by every wave right after
+  // the K-step barrier, the CU's 64 DMA instructions of a stage queue at the
+  // texture unit together for about 1000 cycles, and a wave cannot issue
+  // MFMAs behind its queued instructions.  Paired launches: down GEMM L
+  // 179 -> 172 us, dgrad L 244 -> 227 us, XL128 510 -> 472 us.  The gather +
+  // gate/up kernel keeps the plain order: there the later issue left it
+  // short of registers (epilogue spills) and no faster.
+  constexpr bool STAGGER = NW == 8 && STAGES == 2 && KIND != KIND_GATHER_SWIGLU;
   static_assert(NW == 4 || NW == 8, "4 or 8 waves");
   static_assert(BN == 128 || BN == 256, "BN is 128 or 256");
   static_assert(A_INSTR >= 1 && B_INSTR >= 1 && NB >= 1 && (KIND != KIND_GATHER_SWIGLU || NB % 2 == 0), "tile split");
@@ -1142,7 +1151,9 @@ __global__ __launch_bounds__(NW * 64, NW == 4 ? 2 : 1) void mgemm_dma_kernel(con
         const int gs = g0 + kt;
         wait_stages<PER, STAGES - 2>(min(STAGES - 2, issued - gs - 1));
         barrier_lds();
-        if (issued == gs + STAGES - 1) issue_next();
+        const bool late = STAGGER && wave >= NW / 2 && MBV > 0;
+        const bool due = issued == gs + STAGES - 1;
+        if (due && !late) issue_next();
         if constexpr (MBV > 0) {
           const char* la = smem + (gs % STAGES) * STAGE_BYTES;
           const char* lb = la + A_BYTES;
@@ -1170,6 +1181,7 @@ __global__ __launch_bounds__(NW * 64, NW == 4 ? 2 : 1) void mgemm_dma_kernel(con
             for (int b = 0; b < NB; ++b)
 #pragma unroll
               for (int a = 0; a < MBV; ++a) acc[b][a] = TR::mfma32(fw[s & 1][b], fa[s & 1][a], acc[b][a]);
+            if (s == 0 && due && late) issue_next();
           }
         }
       }
@@ -1183,7 +1195,9 @@ __global__ __launch_bounds__(NW * 64, NW == 4 ? 2 : 1) void mgemm_dma_kernel(con
         const int gs = g0 + kt;
         wait_stages<PER, STAGES - 2>(min(STAGES - 2, issued - gs - 1));
         barrier_lds();
-        if (issued == gs + STAGES - 1) issue_next();
+        const bool late = STAGGER && wave >= NW / 2;
+        const bool due = issued == gs + STAGES - 1;
+        if (due && !late) issue_next();
         const char* la = smem + (gs % STAGES) * STAGE_BYTES;
         const char* lb = la + A_BYTES;
         u32x4 fw[2][NB], fa[2][MBH];
@@ -1210,6 +1224,7 @@ __global__ __launch_bounds__(NW * 64, NW == 4 ? 2 : 1) void mgemm_dma_kernel(con
           for (int b = 0; b < NB; ++b)
 #pragma unroll
             for (int a = 0; a < MBH; ++a) acc[b][a] = TR::mfma32(fw[s & 1][b], fa[s & 1][a], acc[b][a]);
+          if (s == 0 && due && late) issue_next();
         }
       }
     } else {
@@ -1619,10 +1634,15 @@ __global__ __launch_bounds__(NW * 64, 1) void wgrad_dma8_kernel(const uint16_t* 
 #pragma unroll
     for (int st = 0; st < STAGES - 1; ++st)
       if (st < nk) issue(st, st);
+    // 2-stage ring: the second half of the waves issues its share of a stage
+    // after its first sub-step of MFMAs (see mgemm_dma_kernel's STAGGER)
+    constexpr bool STAGGER = NW == 8 && STAGES == 2;
+    const bool late = STAGGER && wave >= NW / 2;
     for (int kt = 0; kt < nk; ++kt) {
       wait_stages<PER, STAGES - 2>(min(STAGES - 2, nk - 1 - kt));
       barrier_lds();
-      if (kt + STAGES - 1 < nk) issue(kt + STAGES - 1, (kt + STAGES - 1) % STAGES);
+      const bool due = kt + STAGES - 1 < nk;
+      if (due && !late) issue(kt + STAGES - 1, (kt + STAGES - 1) % STAGES);
       const char* la = smem + (kt % STAGES) * STAGE_BYTES;
       const char* lb = la + TA_BYTES;
       u32x4 fb[2][NB], fa[2][MB];
@@ -1640,6 +1660,7 @@ __global__ __launch_bounds__(NW * 64, 1) void wgrad_dma8_kernel(const uint16_t* 
         for (int b = 0; b < NB; ++b)
 #pragma unroll
           for (int a = 0; a < MB; ++a) acc[b][a] = TR::mfma32(fb[sub & 1][b], fa[sub & 1][a], acc[b][a]);
+        if (sub == 0 && due && late) issue(kt + STAGES - 1, (kt + STAGES - 1) % STAGES);
       }
     }
 
