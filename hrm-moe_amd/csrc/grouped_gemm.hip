@@ -1401,7 +1401,12 @@ __global__ __launch_bounds__(NW * 64, NW == 4 ? 2 : 1) void mgemm_dma_kernel(con
 // The grid holds min(E, M) x cblk_n workgroups: workgroup group j serves the
 // j-th expert that has rows (found with a ballot over tokens_per_expert), so
 // at a token or two no workgroups are spent on the many empty experts.
-template <typename TR, int KIND, int NRB, int PD>
+// CPW > 0: each wave loads exactly CPW 32-wide K chunks (its own, the last
+// one repeated past its range), all in flight at once, and the loop is
+// unrolled so every MFMA waits only for its own chunk.  In the PD ring the
+// loop-carried loads made each iteration wait for every load in flight, one
+// memory round trip per PD chunks.  CPW = 0 keeps the ring (large K).
+template <typename TR, int KIND, int NRB, int PD, int CPW = 0>
 __global__ __launch_bounds__(256) void mgemm_skinny_kernel(const uint16_t* __restrict__ A,
                                                            const int32_t* __restrict__ gather,
                                                            const uint16_t* __restrict__ W, uint16_t* __restrict__ C,
@@ -1466,7 +1471,29 @@ __global__ __launch_bounds__(256) void mgemm_skinny_kernel(const uint16_t* __res
       ag[rb] = floatx4{0.f, 0.f, 0.f, 0.f};
       au[rb] = floatx4{0.f, 0.f, 0.f, 0.f};
     }
-    if (kc1 > kc0) {
+    if constexpr (CPW > 0) {
+      if (kc1 > kc0) {
+        u32x4 bg[CPW], bu[CPW], bx[CPW][NRB];
+#pragma unroll
+        for (int u = 0; u < CPW; ++u) {
+          const int k = (kc0 + u < kc1 ? kc0 + u : kc1 - 1) * 32;
+          bg[u] = ld16(wg + k);
+          if constexpr (SW) bu[u] = ld16(wu + k);
+#pragma unroll
+          for (int rb = 0; rb < NRB; ++rb) bx[u][rb] = ld16(xr[rb] + k);
+        }
+#pragma unroll
+        for (int u = 0; u < CPW; ++u) {
+          if (kc0 + u < kc1) {
+#pragma unroll
+            for (int rb = 0; rb < NRB; ++rb) {
+              ag[rb] = TR::mfma16(bg[u], bx[u][rb], ag[rb]);
+              if constexpr (SW) au[rb] = TR::mfma16(bu[u], bx[u][rb], au[rb]);
+            }
+          }
+        }
+      }
+    } else if (kc1 > kc0) {
       u32x4 bg[PD], bu[PD], bx[PD][NRB];
       // loads of chunk kc into ring slot u; chunks past the wave's range reload its last one
       auto load = [&](int u, int kc) __attribute__((always_inline)) {
@@ -2032,15 +2059,28 @@ int dispatch_mgemm_t(const void* A, const int32_t* gather, const void* W, const 
       const int cblk_n = N / 16;
       const int groups = (int)(M < (int64_t)E ? M : (int64_t)E);  // at most one group per expert with rows
       const dim3 grid((unsigned)(groups * cblk_n));
-      // 4 K chunks in flight per wave (8 measured slower at T = 1: 55.7 against 52.7 us per layer)
-#define HRM_SK(NRB_)                                                                                          \
-  HRM_LAUNCH((mgemm_skinny_kernel<TR, KIND, NRB_, 4>), grid, dim3(256), 0, stream, (const uint16_t*)A, gather, \
-             (const uint16_t*)W, (uint16_t*)C, tpe, E, (int)M, N, K, cblk_n)
+#define HRM_SK(NRB_, CPW_)                                                                                  \
+  HRM_LAUNCH((mgemm_skinny_kernel<TR, KIND, NRB_, 4, CPW_>), grid, dim3(256), 0, stream, (const uint16_t*)A, \
+             gather, (const uint16_t*)W, (uint16_t*)C, tpe, E, (int)M, N, K, cblk_n)
+      // chunks per wave (4 waves split K in 32-wide chunks): all of a wave's loads in flight at once up to 16
+      const int need = (K / 32 + 3) / 4;
+      const int cpw = need <= 4 ? 4 : (need <= 8 ? 8 : (need <= 12 ? 12 : (need <= 16 ? 16 : 0)));
       const int nrb = M <= (int64_t)E * 4 ? 1 : 2;  // up to 4 rows per expert on average: one 16-row block per pass
-      snprintf(g_last_kernel[KIND], sizeof(g_last_kernel[KIND]), "mgemm_skinny_kernel<%s, %d, %d, 4>", tr_name<TR>(),
-               KIND, nrb);
-      if (nrb == 1) HRM_SK(1);
-      else HRM_SK(2);
+      snprintf(g_last_kernel[KIND], sizeof(g_last_kernel[KIND]), "mgemm_skinny_kernel<%s, %d, %d, 4, %d>",
+               tr_name<TR>(), KIND, nrb, cpw);
+      if (nrb == 1) {
+        if (cpw == 4) HRM_SK(1, 4);
+        else if (cpw == 8) HRM_SK(1, 8);
+        else if (cpw == 12) HRM_SK(1, 12);
+        else if (cpw == 16) HRM_SK(1, 16);
+        else HRM_SK(1, 0);
+      } else {
+        if (cpw == 4) HRM_SK(2, 4);
+        else if (cpw == 8) HRM_SK(2, 8);
+        else if (cpw == 12) HRM_SK(2, 12);
+        else if (cpw == 16) HRM_SK(2, 16);
+        else HRM_SK(2, 0);
+      }
 #undef HRM_SK
       return HRM_MOE_OK;
     }
