@@ -41,6 +41,12 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 METRIC = "MoE FFN ms/layer + active TFLOP/s (% bf16 MFMA peak), L 64x8, 16k tokens"
+# the same figures for the other layer-forward shapes (parity-test and comparison workloads)
+LAYER_METRICS = {
+    "l64x8": METRIC,
+    "xl_skew": "MoE FFN ms/layer + active TFLOP/s (% bf16 MFMA peak), XL 64x8 skewed loads, 16k tokens",
+    "xl128": "MoE FFN ms/layer + active TFLOP/s (% bf16 MFMA peak), XL 128x8, 32k tokens",
+}
 PEAK_BF16_TFLOPS = 2500.0  # MI355X dense bf16 MFMA (published)
 PEAK_HBM_GBS = 8000.0
 
@@ -253,6 +259,40 @@ def cpu_baseline(t, h, e, i, k, bias_std=0.0, runs=5, legs=()):
     return out
 
 
+def decode_gate_up_us(layers, xs, dispatches, reps):
+    """Average duration (us) of the gate_up kernel alone at a decode size, and its instantiation.
+
+    One HIP graph holds one launch per weight copy, back to back; HIP events on
+    the replaying stream bracket ``reps`` replays.
+    """
+    from hrm_moe_amd import _lib, ops
+
+    weights = [layer.experts.gate_up_weight.to(x.dtype) for layer, x in zip(layers, xs)]
+    with torch.no_grad():
+        side = torch.cuda.Stream()  # default priority
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            for x, d, w in zip(xs, dispatches, weights):
+                ops.gate_up_swiglu(x, d, w)
+        torch.cuda.current_stream().wait_stream(side)
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            for x, d, w in zip(xs, dispatches, weights):
+                ops.gate_up_swiglu(x, d, w)
+    kernel = _lib.last_gemm_kernel(_lib.GEMM_KIND_GATE_UP)
+    for _ in range(3):
+        graph.replay()
+    torch.cuda.synchronize()
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(reps):
+        graph.replay()
+    end.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) * 1e3 / (reps * len(xs)), kernel
+
+
 def run_decode(args, hrm, dev):
     """Decode-size layer latency: graph replays rotating over weight copies that together exceed the MALL."""
     from hrm_moe_amd import ops
@@ -285,15 +325,22 @@ def run_decode(args, hrm, dev):
     us_copy = timed(xs)
     # algorithmic bytes: the touched experts' weights, the tokens in and out, the router weight
     with torch.no_grad():
-        distinct = []
+        dispatches = []
         for c in range(copies):
             logits = torch.nn.functional.linear(xs[c], layers[c].gate.weight)
-            distinct.append(int(torch.unique(ops.router_topk(logits, k, True, torch.bfloat16)[2]).numel()))
+            dispatches.append(ops.router_topk_dispatch(logits, k, True, torch.bfloat16, want_probs=False)[3])
+    distinct = [int((d.tokens_per_expert > 0).sum().item()) for d in dispatches]
     touched = statistics.fmean(distinct)
     nbytes = touched * 3 * h * i * 2 + 2 * t * h * 2 + h * e * 2
     gbs = nbytes / (us * 1e-6) / 1e9
     log(f"decode T={t}: {us:.2f} us/layer ({us_copy:.2f} with the input copy), {touched:.1f} experts touched, "
         f"{nbytes / 1e6:.1f} MB, {gbs:.0f} GB/s")
+    # dominant kernel: the fused gather + gate_up + SwiGLU, timed alone from a graph of back-to-back
+    # launches over the weight copies (HIP events on the stream the graph is replayed on)
+    gu_us, gu_kernel = decode_gate_up_us(layers, xs, dispatches, max(args.steps, 20))
+    gu_bytes = statistics.fmean(n * 2 * i * h * 2 for n in distinct) + t * k * (h + i) * 2
+    gu_gbs = gu_bytes / (gu_us * 1e-6) / 1e9
+    log(f"decode T={t}: gate_up kernel {gu_kernel} {gu_us:.2f} us, {gu_bytes / 1e6:.1f} MB, {gu_gbs:.0f} GB/s")
     result = {
         "metric": f"MoE FFN decode latency, XL 64x8 (H={h}, E={e}, I={i}, top-{k}), {t} tokens",
         "value": round(us, 3),
@@ -312,10 +359,17 @@ def run_decode(args, hrm, dev):
                                f"input buffer (us_with_input_copy: copied in each step)",
                    "tokens": t, "hidden": h, "experts": e, "inter": i, "top_k": k, "weight_copies": copies},
         "us_with_input_copy": round(us_copy, 3),
-        "roofline": {"kernel": "whole layer (weight streaming)", "bound": "hbm", "achieved": round(gbs, 1),
-                     "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": None,
-                     "bytes_per_step": int(nbytes), "experts_touched": touched},
+        "layer_hbm": {"bytes_per_step": int(nbytes), "achieved_gbs": round(gbs, 1),
+                      "frac": round(gbs / PEAK_HBM_GBS, 4), "experts_touched": touched},
+        "roofline": {"kernel": f"{gu_kernel} (fused gather + gate_up GEMM + SwiGLU)", "bound": "hbm",
+                     "achieved": round(gu_gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                     "frac": round(gu_gbs / PEAK_HBM_GBS, 4), "traffic": None,
+                     "bytes_per_launch": int(gu_bytes), "avg_launch_us": round(gu_us, 3)},
     }
+    traffic = read_traffic(f"gate_up_swiglu_{args.workload}_traffic.txt", gu_kernel)
+    if traffic is not None:
+        result["roofline"]["traffic"] = traffic["fetch_bytes_per_launch"] + traffic["write_bytes_per_launch"]
+        result["roofline"]["traffic_detail"] = traffic
     if not args.no_cpu_baseline:
         cb = cpu_baseline(t, h, e, i, k, runs=5)
         result["cpu_baseline"] = {"value": round(cb["ms_per_layer"] * 1e3, 1), "unit": "us/layer",
@@ -538,7 +592,7 @@ def main():
         f"{100 * tflops / PEAK_BF16_TFLOPS:.1f}% of bf16 peak")
 
     result = {
-        "metric": METRIC,
+        "metric": LAYER_METRICS[args.workload],
         "value": round(tflops, 2),
         "unit": "TFLOP/s",
         "n_gpus": 1,
