@@ -1988,8 +1988,10 @@ int launch_mgemm_dma(const void* A, const int32_t* gather, const void* W, const 
 // stages of 64-wide K steps (128 KB of LDS) when experts average at least 256
 // rows and the weight rows split into whole 256-row tiles (the gate/up kernel
 // also supports a last half tile of 64 gate + 64 up rows when selected
-// explicitly); 32 x 256 tiles (4 waves along N, 4 stages, 144 KB) when
-// experts average at most 16 rows; otherwise 128 x 128
+// explicitly); when experts average at most 16 rows, 32 x 256 tiles (4 waves
+// along N, 4 stages, 144 KB) for gate/up and 32 x 128 tiles (5 stages, 100 KB)
+// for the down projection (a 32 x 128 choice for gate/up runs 32 x 256);
+// otherwise 128 x 128
 // tiles, 4 waves, 2 stages (64 KB of LDS, two workgroups per CU).  The large
 // tile halves LDS and L2 traffic per flop; the small one wastes less on ragged
 // experts and on widths that are not multiples of 256.
@@ -1999,7 +2001,8 @@ struct MCfg {
   int bm, bn, stages, waves, bk;
 };
 bool mcfg_built(const MCfg& c) {
-  if (c.bm == 32) return c.bn == 256 && c.waves == 4 && c.bk == 64 && c.stages == 4;
+  if (c.bm == 32)
+    return c.waves == 4 && c.bk == 64 && ((c.bn == 256 && c.stages == 4) || (c.bn == 128 && (c.stages == 4 || c.stages == 5)));
   if (c.bm == 256 && c.bn == 128 && c.waves == 4) return c.bk == 32 && (c.stages == 2 || c.stages == 3);
   if (c.bm == 128 && c.bn == 128 && c.waves == 4)
     return (c.bk == 64 && (c.stages == 2 || c.stages == 3)) || (c.bk == 32 && (c.stages == 4 || c.stages == 5));
@@ -2022,14 +2025,17 @@ MCfg mgemm_cfg(int64_t M, int E, int64_t w_rows, bool gate_up, bool nn = false) 
   // multiple of 256: at L's dact (N = 448) they measured 203 us against 272 us
   // for 128 x 128 tiles, whose higher LDS and DMA traffic per flop costs more
   // than the idle columns of the last N tile.
-  (void)gate_up;
   if (M >= (int64_t)E * 256 && (nn || w_rows % 256 == 0)) return MCfg{256, 256, 2, 8, 64};
   // Decode sizes (experts average at most 16 rows): the GEMM streams weights,
   // and 32-row tiles leave LDS for 4 stages of 256 weight rows (3 K steps in
   // flight).  Decode layer at H = 1536, I = 512: T = 8 88.8 -> 82.8 us,
   // T = 64 104.8 -> 100.8 us; at T = 256 (32 rows per expert) 128 x 128 stays
-  // faster (111.5 against 120.1 us).
-  if (!nn && M <= (int64_t)E * 16) return MCfg{32, 256, 4, 4, 64};
+  // faster (111.5 against 120.1 us).  The down projection takes 32 x 128
+  // tiles with 5 stages: twice the workgroups, each streaming half the weight
+  // rows, so all CUs stream at T = 8 (255 -> 510 tiles; layer 62.6 -> 61.3 us,
+  // T = 64 85.0 -> 83.8 us).  The gate/up pair needs two 32-column blocks per
+  // wave, so its N tile stays 256.
+  if (!nn && M <= (int64_t)E * 16) return gate_up ? MCfg{32, 256, 4, 4, 64} : MCfg{32, 128, 5, 4, 64};
   return MCfg{128, 128, 2, 4, 64};
 }
 
@@ -2095,6 +2101,12 @@ int dispatch_mgemm_t(const void* A, const int32_t* gather, const void* W, const 
   }
 #define HRM_MG(BM_, BN_, ST_, NW_, BK_) \
   return launch_mgemm_dma<TR, KIND, BM_, BN_, ST_, NW_, BK_>(A, gather, W, tpe, M, N, K, E, a_rows, C, workspace, stream)
+  if constexpr (KIND != KIND_GATHER_SWIGLU) {
+    if (c.bm == 32 && c.bn == 128) {
+      if (c.stages == 5) HRM_MG(32, 128, 5, 4, 64);
+      HRM_MG(32, 128, 4, 4, 64);
+    }
+  }
   if (c.bm == 32) HRM_MG(32, 256, 4, 4, 64);
   if (c.bm == 256 && c.bn == 128) {
     if (c.stages == 2) HRM_MG(256, 128, 2, 4, 32);

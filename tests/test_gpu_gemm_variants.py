@@ -4,7 +4,7 @@ The wgrad kernels (8-wave 256 x 256 and the 4-wave 128 x 128 ones with 2 or 3
 stages, HRM_MOE_WGRAD_STAGES) are checked the same way.
 
 The variants differ in tile shape (128 x 128 with 4 waves, 256 x 256 with 8
-waves, 32 x 256 with 4 waves along N for decode sizes), pipeline depth and K
+waves, 32 x 256 and 32 x 128 with 4 waves along N for decode sizes), pipeline depth and K
 step (64 or 32), and the gate/up kernel's
 256 x 256 variant runs its last N tile as a half tile when the width is an odd
 multiple of 64.  All of them accumulate each output over K in the same order
@@ -23,7 +23,8 @@ from conftest import lib_env
 pytestmark = pytest.mark.gpu
 
 VARIANTS = ["128x128x2x4x64", "128x128x3x4x64", "128x128x4x4x32", "128x128x5x4x32",
-            "256x128x2x4x32", "256x128x3x4x32", "256x256x2x8x64", "256x256x4x8x32", "32x256x4x4x64"]
+            "256x128x2x4x32", "256x128x3x4x32", "256x256x2x8x64", "256x256x4x8x32", "32x256x4x4x64",
+            "32x128x4x4x64", "32x128x5x4x64"]
 
 
 def _ragged(seed, m, e):
