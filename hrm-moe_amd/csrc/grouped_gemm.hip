@@ -777,6 +777,10 @@ template <int CPOL = 0>
 __device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t r, char* lds_dst, uint32_t voff, uint32_t soff) {
   __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (HRM_LDS void*)lds_dst, 16, voff, soff, 0, CPOL);
 }
+// 4 bytes per lane straight into LDS (lane l's dword at lds_dst + 4 l)
+__device__ __forceinline__ void dma4(__amdgpu_buffer_rsrc_t r, char* lds_dst, uint32_t voff) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (HRM_LDS void*)lds_dst, 4, voff, 0, 0, 0);
+}
 template <int N>
 __device__ __forceinline__ void wait_vmcnt() {
   static_assert(N >= 0 && N < 64, "vmcnt field is 6 bits");
@@ -909,8 +913,12 @@ __global__ __launch_bounds__(NW * 64, NW == 4 ? 2 : 1) void mgemm_dma_kernel(con
   static_assert(STAGES >= 2 && STAGES <= 5, "2..5 stages");
   // the ring plus the tile plan (3 ints per expert, dynamic) must fit one
   // workgroup's 160 KB of LDS, or the dispatch is rejected
-  static_assert(STAGES * STAGE_BYTES + 3 * 4 * kMaxExperts <= 160 * 1024, "LDS budget exceeds 160 KB");
-  __shared__ __attribute__((aligned(1024))) char smem[STAGES * STAGE_BYTES];
+  static_assert(STAGES * STAGE_BYTES + 3 * 4 * kMaxExperts +
+                        (KIND == KIND_GATHER_SWIGLU ? NW * A_INSTR * 64 * 4 : 0) <= 160 * 1024,
+                "LDS budget exceeds 160 KB");
+  // gate/up kernel: the ring, then the gathered source rows of the prefetched tile
+  constexpr int GIDX_BYTES = KIND == KIND_GATHER_SWIGLU ? NW * A_INSTR * 64 * 4 : 0;
+  __shared__ __attribute__((aligned(1024))) char smem[STAGES * STAGE_BYTES + GIDX_BYTES];
   extern __shared__ int plan_lds[];  // [3][E]: row start, row end, inclusive M-tile prefix
 
   const int tid = threadIdx.x;
@@ -990,13 +998,29 @@ __global__ __launch_bounds__(NW * 64, NW == 4 ? 2 : 1) void mgemm_dma_kernel(con
   uint32_t pf_src[A_INSTR];
 #pragma unroll
   for (int i = 0; i < A_INSTR; ++i) pf_src[i] = 0;
+  // Gathered source rows of the prefetched tile (gate/up kernel): DMA'd into
+  // LDS, one dword per lane, and read back when the tile is taken, a whole
+  // tile later.  Loaded into registers, they were copied at once into the
+  // registers that carry them across the loop, and that copy waited for the
+  // load, and so for every DMA in flight, at each tile switch.  By the time
+  // they are read, the K-step waits (vmcnt, which counts in issue order)
+  // have covered their DMA.
+  constexpr bool GIDX = KIND == KIND_GATHER_SWIGLU;
+  uint32_t* const gidx = reinterpret_cast<uint32_t*>(smem + STAGES * STAGE_BYTES);  // [NW][A_INSTR][64]
+  const __amdgpu_buffer_rsrc_t rG = make_rsrc(gather, GIDX ? (uint32_t)M * 4u : 0u);
 
   auto load_src = [&](const MTile& m) __attribute__((always_inline)) {
 #pragma unroll
     for (int i = 0; i < A_INSTR; ++i) {
       int r = m.row_start + wave * A_ROWS + i * RPIK + lrowk;
       r = r < m.row_end ? r : m.row_end - 1;
-      pf_src[i] = KIND == KIND_GATHER_SWIGLU ? (uint32_t)gather[r] : (uint32_t)r;
+      if constexpr (GIDX) {
+        // the previous tile's indices have been read back (that ds_read is done) before the DMA overwrites them
+        if (i == 0) __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
+        dma4(rG, reinterpret_cast<char*>(gidx + (wave * A_INSTR + i) * 64), (uint32_t)r * 4u);
+      } else {
+        pf_src[i] = (uint32_t)r;
+      }
     }
   };
   auto prefetch = [&](int seq) __attribute__((always_inline)) {
@@ -1040,7 +1064,8 @@ __global__ __launch_bounds__(NW * 64, NW == 4 ? 2 : 1) void mgemm_dma_kernel(con
     for (int i = 0; i < A_INSTR; ++i) {
       const int row = wave * A_ROWS + i * RPIK + lrowk;
       const int lc = lchk ^ kcp_swz<PK>(row);
-      a_off[i] = (pf_src[i] * (uint32_t)K + lc * 8) * 2;
+      const uint32_t src = GIDX ? gidx[(wave * A_INSTR + i) * 64 + lane] : pf_src[i];
+      a_off[i] = (src * (uint32_t)K + lc * 8) * 2;
     }
     if constexpr (KIND == KIND_NN) {
       iss_n0 = nt * BN;
@@ -1111,6 +1136,7 @@ __global__ __launch_bounds__(NW * 64, NW == 4 ? 2 : 1) void mgemm_dma_kernel(con
   // first tile
   prefetch(0);
   if (pf_t < 0) return;
+  if constexpr (GIDX) wait_vmcnt<0>();  // its gathered source rows are in LDS
   take_prefetched();
   iss_valid = true;
   prefetch(1);
