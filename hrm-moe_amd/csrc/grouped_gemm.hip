@@ -848,6 +848,31 @@ __device__ __forceinline__ u32x4 bload16(__amdgpu_buffer_rsrc_t r, uint32_t voff
 // GEMM at L (131072 x 1280 x 448) measured 177 against 204 us, and the L
 // training step (dgrad and wgrad outputs too) 2384 against 2398 us.
 constexpr int kCpolNT = 2;
+// The same DMA issued as inline assembly, for kernels that read their tiles
+// with ds_read_b64_tr_b16.  The compiler treats that read as possibly
+// aliasing any LDS written by a DMA it knows of, and put an
+// s_waitcnt vmcnt(0) before the first transposed read of every K step: each
+// step then waited for the DMA of the step after it, which the ring issues
+// just before, so no DMA overlapped any MFMA.  DMAs it cannot see are not
+// tracked; these kernels order their DMAs with explicit vmcnt waits and
+// barriers anyway.  Loads the compiler issues itself are still waited for
+// correctly: extra operations in flight only make its vmcnt counts stricter.
+// The LDS address goes to m0 and the scalar offset to an SGPR, so both must be
+// wave-uniform, as they are at every call.  No other code in these kernels
+// uses m0 (checked in the generated code: only these writes of it appear).
+template <int CPOL = 0>
+__device__ __forceinline__ void dma16t(__amdgpu_buffer_rsrc_t r, char* lds_dst, uint32_t voff, uint32_t soff) {
+  const uint32_t lds = __builtin_amdgcn_readfirstlane((uint32_t)(size_t)(HRM_LDS void*)lds_dst);
+  soff = __builtin_amdgcn_readfirstlane(soff);
+  if constexpr (CPOL == kCpolNT)
+    asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, %3 offen nt lds" ::"s"(lds), "v"(voff), "s"(r),
+                 "s"(soff)
+                 : "memory", "m0");
+  else
+    asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds" ::"s"(lds), "v"(voff), "s"(r),
+                 "s"(soff)
+                 : "memory", "m0");
+}
 __device__ __forceinline__ void bstore8(__amdgpu_buffer_rsrc_t r, uint32_t voff, u32x2 v) {
   __builtin_amdgcn_raw_buffer_store_b64(v, r, voff, 0, 0);
 }
@@ -1113,12 +1138,17 @@ __global__ __launch_bounds__(NW * 64, NW == 4 ? 2 : 1) void mgemm_dma_kernel(con
     char* sa = smem + (issued % STAGES) * STAGE_BYTES;
     char* sb = sa + A_BYTES;
     const uint32_t ka = (uint32_t)iss_step * (BK * 2);
+    if constexpr (KIND == KIND_NN) {  // the W tile is read transposed: DMA the compiler cannot see
 #pragma unroll
-    for (int i = 0; i < A_INSTR; ++i) dma16(rA, sa + (wave * A_ROWS + i * RPIK) * PK, a_off[i], ka);
+      for (int i = 0; i < A_INSTR; ++i) dma16t(rA, sa + (wave * A_ROWS + i * RPIK) * PK, a_off[i], ka);
+    } else {
+#pragma unroll
+      for (int i = 0; i < A_INSTR; ++i) dma16(rA, sa + (wave * A_ROWS + i * RPIK) * PK, a_off[i], ka);
+    }
     if constexpr (KIND == KIND_NN) {
       const uint32_t kb = (uint32_t)iss_step * BK * (uint32_t)N * 2;
 #pragma unroll
-      for (int i = 0; i < B_INSTR; ++i) dma16(rB, sb + (wave * NN_KR + i * NN_RPI) * (BN * 2), b_off[i], kb);
+      for (int i = 0; i < B_INSTR; ++i) dma16t(rB, sb + (wave * NN_KR + i * NN_RPI) * (BN * 2), b_off[i], kb);
     } else {
       // 32-row tiles run at decode sizes, where each expert's weight rows are
       // read once: non-temporal loads (decode layer T = 8 82.9 -> 73.8 us,
@@ -1663,15 +1693,21 @@ __global__ __launch_bounds__(NW * 64, 1) void wgrad_dma8_kernel(const uint16_t* 
       char* sb = sa + TA_BYTES;
       const uint32_t sofa = (uint32_t)kt * kBK * (uint32_t)Na * 2;
       const uint32_t sofb = (uint32_t)kt * kBK * (uint32_t)Nb * 2;
+      // gathered B rows (GB): the source-row loads are the compiler's and it
+      // waits for them right away, which the DMA the compiler knows of
+      // overlaps better (measured); the plain wgrad takes the invisible DMA
 #pragma unroll
-      for (int i = 0; i < IA; ++i) dma16(rA, sa + (wave * KR + i * RPI_A) * (BA * 2), oa[i], sofa);
+      for (int i = 0; i < IA; ++i) {
+        if constexpr (GB) dma16(rA, sa + (wave * KR + i * RPI_A) * (BA * 2), oa[i], sofa);
+        else dma16t(rA, sa + (wave * KR + i * RPI_A) * (BA * 2), oa[i], sofa);
+      }
 #pragma unroll
       for (int i = 0; i < IB; ++i) {
         if constexpr (GB)
           dma16(rB, sb + (wave * KR + i * RPI_B) * (BB * 2),
                 gi[i] >= 0 ? (uint32_t)gi[i] * (uint32_t)Nb * 2 + ob[i] : 0x80000000u, 0);
         else
-          dma16(rB, sb + (wave * KR + i * RPI_B) * (BB * 2), ob[i], sofb);
+          dma16t(rB, sb + (wave * KR + i * RPI_B) * (BB * 2), ob[i], sofb);
       }
       if constexpr (GB) load_gi(kt + 1);
     };
@@ -1854,12 +1890,14 @@ __global__ __launch_bounds__(kThreads, 1) void wgrad_dma_kernel(const uint16_t* 
       const uint32_t sofb = (uint32_t)kt * kBK * (uint32_t)Nb * 2;
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        dma16(rA, sa + (wave * 16 + i * 4) * 256, oa[i], sofa);
-        if constexpr (GB)
+        if constexpr (GB) {  // as in the 8-wave kernel: gathered B keeps the DMA the compiler knows of
+          dma16(rA, sa + (wave * 16 + i * 4) * 256, oa[i], sofa);
           dma16(rB, sb + (wave * 16 + i * 4) * 256,
                 gi[i] >= 0 ? (uint32_t)gi[i] * (uint32_t)Nb * 2 + ob[i] : 0x80000000u, 0);
-        else
-          dma16(rB, sb + (wave * 16 + i * 4) * 256, ob[i], sofb);
+        } else {
+          dma16t(rA, sa + (wave * 16 + i * 4) * 256, oa[i], sofa);
+          dma16t(rB, sb + (wave * 16 + i * 4) * 256, ob[i], sofb);
+        }
       }
       if constexpr (GB) load_gi(kt + 1);
     };
