@@ -777,6 +777,12 @@ template <int CPOL = 0>
 __device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t r, char* lds_dst, uint32_t voff, uint32_t soff) {
   __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (HRM_LDS void*)lds_dst, 16, voff, soff, 0, CPOL);
 }
+// 4 bytes per lane into LDS (lane l's dword at lds_dst + 4 l), as inline assembly like dma16t
+__device__ __forceinline__ void dma4t(__amdgpu_buffer_rsrc_t r, char* lds_dst, uint32_t voff) {
+  const uint32_t lds = __builtin_amdgcn_readfirstlane((uint32_t)(size_t)(HRM_LDS void*)lds_dst);
+  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dword %1, %2, 0 offen lds" ::"s"(lds), "v"(voff), "s"(r)
+               : "memory", "m0");
+}
 // 4 bytes per lane straight into LDS (lane l's dword at lds_dst + 4 l)
 __device__ __forceinline__ void dma4(__amdgpu_buffer_rsrc_t r, char* lds_dst, uint32_t voff) {
   __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (HRM_LDS void*)lds_dst, 4, voff, 0, 0, 0);
@@ -1638,6 +1644,8 @@ __global__ __launch_bounds__(NW * 64, 1) void wgrad_dma8_kernel(const uint16_t* 
   static_assert(STAGES * STAGE_BYTES <= 160 * 1024, "LDS ring exceeds 160 KB");
   __shared__ __attribute__((aligned(1024))) char smem[STAGES * STAGE_BYTES];
   __shared__ int s_tile;
+  __shared__ uint32_t s_gi[GB ? NW : 1][GB ? IB : 1][64];
+  const __amdgpu_buffer_rsrc_t rI = make_rsrc(b_index, GB ? 0x7ffffffcu : 0u);
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wave / WGN, wn = wave % WGN;
@@ -1663,7 +1671,9 @@ __global__ __launch_bounds__(NW * 64, 1) void wgrad_dma8_kernel(const uint16_t* 
     const __amdgpu_buffer_rsrc_t rB =
         GB ? make_rsrc(B, b_bytes) : make_rsrc(B + (int64_t)rs * Nb, (uint32_t)(re - rs) * (uint32_t)Nb * 2);
     uint32_t oa[IA], ob[IB];
-    int gi[IB];  // GB: source row of each of this lane's B k rows in the next step to issue, -1 past the expert
+    // GB: source rows of this wave's B k rows for the next step to issue, DMA'd
+    // into s_gi (one dword per lane) during the step before and read back at
+    // the issue; the step's vmcnt(0) wait (2-stage ring) covers that DMA
 #pragma unroll
     for (int i = 0; i < IA; ++i) {
       const int kr = wave * KR + i * RPI_A + lane / LPR_A;
@@ -1680,32 +1690,34 @@ __global__ __launch_bounds__(NW * 64, 1) void wgrad_dma8_kernel(const uint16_t* 
       cb = cb < Nb ? cb : Nb - 8;
       ob[i] = GB ? (uint32_t)cb * 2 : ((uint32_t)kr * (uint32_t)Nb + (uint32_t)cb) * 2;
     }
+    auto gi_row = [&](int kt, int i) __attribute__((always_inline)) {
+      return rs + kt * kBK + wave * KR + i * RPI_B + lane / LPR_B;
+    };
     auto load_gi = [&](int kt) __attribute__((always_inline)) {
 #pragma unroll
       for (int i = 0; i < IB; ++i) {
-        const int row = rs + kt * kBK + wave * KR + i * RPI_B + lane / LPR_B;
-        gi[i] = row < re ? b_index[row] : -1;
+        const int row = gi_row(kt, i);
+        dma4t(rI, reinterpret_cast<char*>(&s_gi[wave][i][0]), (uint32_t)(row < re ? row : re - 1) * 4u);
       }
     };
-    if constexpr (GB) load_gi(0);
+    if constexpr (GB) {
+      if (nk > 0) {
+        load_gi(0);
+        wait_vmcnt<0>();
+      }
+    }
     auto issue = [&](int kt, int stage) __attribute__((always_inline)) {
       char* sa = smem + stage * STAGE_BYTES;
       char* sb = sa + TA_BYTES;
       const uint32_t sofa = (uint32_t)kt * kBK * (uint32_t)Na * 2;
       const uint32_t sofb = (uint32_t)kt * kBK * (uint32_t)Nb * 2;
-      // gathered B rows (GB): the source-row loads are the compiler's and it
-      // waits for them right away, which the DMA the compiler knows of
-      // overlaps better (measured); the plain wgrad takes the invisible DMA
 #pragma unroll
-      for (int i = 0; i < IA; ++i) {
-        if constexpr (GB) dma16(rA, sa + (wave * KR + i * RPI_A) * (BA * 2), oa[i], sofa);
-        else dma16t(rA, sa + (wave * KR + i * RPI_A) * (BA * 2), oa[i], sofa);
-      }
+      for (int i = 0; i < IA; ++i) dma16t(rA, sa + (wave * KR + i * RPI_A) * (BA * 2), oa[i], sofa);
 #pragma unroll
       for (int i = 0; i < IB; ++i) {
         if constexpr (GB)
-          dma16(rB, sb + (wave * KR + i * RPI_B) * (BB * 2),
-                gi[i] >= 0 ? (uint32_t)gi[i] * (uint32_t)Nb * 2 + ob[i] : 0x80000000u, 0);
+          dma16t(rB, sb + (wave * KR + i * RPI_B) * (BB * 2),
+                 gi_row(kt, i) < re ? s_gi[wave][i][lane] * (uint32_t)Nb * 2 + ob[i] : 0x80000000u, 0);
         else
           dma16t(rB, sb + (wave * KR + i * RPI_B) * (BB * 2), ob[i], sofb);
       }
@@ -1841,6 +1853,8 @@ __global__ __launch_bounds__(kThreads, 1) void wgrad_dma_kernel(const uint16_t* 
   constexpr int PER = 8;  // 4 + 4 loads per wave per stage
   __shared__ __attribute__((aligned(1024))) char smem[STAGES * STAGE_BYTES];
   __shared__ int s_tile;
+  __shared__ uint32_t s_gi[GB ? 4 : 1][GB ? 4 : 1][64];  // [wave][i][lane], as in wgrad_dma8_kernel
+  const __amdgpu_buffer_rsrc_t rI = make_rsrc(b_index, GB ? 0x7ffffffcu : 0u);
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wa = wave >> 1, wb = wave & 1;
@@ -1864,7 +1878,7 @@ __global__ __launch_bounds__(kThreads, 1) void wgrad_dma_kernel(const uint16_t* 
     const __amdgpu_buffer_rsrc_t rB =
         GB ? make_rsrc(B, b_bytes) : make_rsrc(B + (int64_t)rs * Nb, (uint32_t)(re - rs) * (uint32_t)Nb * 2);
     uint32_t oa[4], ob[4];
-    int gi[4];  // GB: source row of each of this lane's B k rows in the next step to issue, -1 past the expert
+    // GB: source rows of this wave's B k rows for the next step to issue, in s_gi (see wgrad_dma8_kernel)
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int kr = wave * 16 + i * 4 + (lane >> 4);
@@ -1875,14 +1889,22 @@ __global__ __launch_bounds__(kThreads, 1) void wgrad_dma_kernel(const uint16_t* 
       oa[i] = ((uint32_t)kr * (uint32_t)Na + (uint32_t)ca) * 2;
       ob[i] = GB ? (uint32_t)cb * 2 : ((uint32_t)kr * (uint32_t)Nb + (uint32_t)cb) * 2;
     }
-    auto load_gi = [&](int kt) {
+    auto gi_row = [&](int kt, int i) __attribute__((always_inline)) {
+      return rs + kt * kBK + wave * 16 + i * 4 + (lane >> 4);
+    };
+    auto load_gi = [&](int kt) __attribute__((always_inline)) {
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const int row = rs + kt * kBK + wave * 16 + i * 4 + (lane >> 4);
-        gi[i] = row < re ? b_index[row] : -1;
+        const int row = gi_row(kt, i);
+        dma4t(rI, reinterpret_cast<char*>(&s_gi[wave][i][0]), (uint32_t)(row < re ? row : re - 1) * 4u);
       }
     };
-    if constexpr (GB) load_gi(0);
+    if constexpr (GB) {
+      if (nk > 0) {
+        load_gi(0);
+        wait_vmcnt<0>();
+      }
+    }
     auto issue = [&](int kt, int stage) {
       char* sa = smem + stage * STAGE_BYTES;
       char* sb = sa + T_BYTES;
@@ -1890,14 +1912,12 @@ __global__ __launch_bounds__(kThreads, 1) void wgrad_dma_kernel(const uint16_t* 
       const uint32_t sofb = (uint32_t)kt * kBK * (uint32_t)Nb * 2;
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        if constexpr (GB) {  // as in the 8-wave kernel: gathered B keeps the DMA the compiler knows of
-          dma16(rA, sa + (wave * 16 + i * 4) * 256, oa[i], sofa);
-          dma16(rB, sb + (wave * 16 + i * 4) * 256,
-                gi[i] >= 0 ? (uint32_t)gi[i] * (uint32_t)Nb * 2 + ob[i] : 0x80000000u, 0);
-        } else {
-          dma16t(rA, sa + (wave * 16 + i * 4) * 256, oa[i], sofa);
+        dma16t(rA, sa + (wave * 16 + i * 4) * 256, oa[i], sofa);
+        if constexpr (GB)
+          dma16t(rB, sb + (wave * 16 + i * 4) * 256,
+                 gi_row(kt, i) < re ? s_gi[wave][i][lane] * (uint32_t)Nb * 2 + ob[i] : 0x80000000u, 0);
+        else
           dma16t(rB, sb + (wave * 16 + i * 4) * 256, ob[i], sofb);
-        }
       }
       if constexpr (GB) load_gi(kt + 1);
     };
