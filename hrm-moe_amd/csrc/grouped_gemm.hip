@@ -934,10 +934,10 @@ __global__ __launch_bounds__(NW * 64, NW == 4 ? 2 : 1) void mgemm_dma_kernel(con
   // the K-step barrier, the CU's 64 DMA instructions of a stage queue at the
   // texture unit together for about 1000 cycles, and a wave cannot issue
   // MFMAs behind its queued instructions.  Paired launches: down GEMM L
-  // 179 -> 172 us, dgrad L 244 -> 227 us, XL128 510 -> 472 us.  The gather +
-  // gate/up kernel keeps the plain order: there the later issue left it
-  // short of registers (epilogue spills) and no faster.
-  constexpr bool STAGGER = NW == 8 && STAGES == 2 && KIND != KIND_GATHER_SWIGLU;
+  // 179 -> 172 us, dgrad L 244 -> 227 us, XL128 510 -> 472 us; gather +
+  // gate/up at XL128 796 -> 780 us, XL-skew 388 -> 382 us (XL-skew training
+  // step 2.874 -> 2.863 ms with the gate/up-saving variant too).
+  constexpr bool STAGGER = NW == 8 && STAGES == 2;
   static_assert(NW == 4 || NW == 8, "4 or 8 waves");
   static_assert(BN == 128 || BN == 256, "BN is 128 or 256");
   static_assert(A_INSTR >= 1 && B_INSTR >= 1 && NB >= 1 && (KIND != KIND_GATHER_SWIGLU || NB % 2 == 0), "tile split");
