@@ -16,7 +16,7 @@ GEMM, from those events on its stream, with the HBM traffic of a committed
 counter summary when it describes the kernel that ran) and the reference's
 eager CPU path timed on the host's cores.
 
-Pass order: the per-op pass runs first, over at least 60 layer forwards.  The
+Pass order: the per-op pass runs first, over at least 100 layer forwards.  The
 GPU's clocks take a few tens of milliseconds of load to settle after idling
 (the first 20 forwards after 5 warmup steps measured 0.67 ms per layer, later
 windows 0.59-0.60 ms), so the headline pass that follows, W warmup steps and
@@ -567,7 +567,7 @@ def main():
     from hrm_moe_amd import _lib
 
     timer = OpTimer(hrm.ops)
-    ms_instr, _ = time_layers(layers, xs, max(args.steps, 60), 2, timer)
+    ms_instr, _ = time_layers(layers, xs, max(args.steps, 100), 2, timer)
     timer.restore()
     gate_up_kernel = _lib.last_gemm_kernel(_lib.GEMM_KIND_GATE_UP)
     ms, wall = time_layers(layers, xs, args.steps, args.warmup)
