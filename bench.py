@@ -16,11 +16,12 @@ GEMM, from those events on its stream, with the HBM traffic of a committed
 counter summary when it describes the kernel that ran) and the reference's
 eager CPU path timed on the host's cores.
 
-Pass order: the per-op pass runs first, over at least 100 layer forwards.  The
-GPU's clocks take a few tens of milliseconds of load to settle after idling
-(the first 20 forwards after 5 warmup steps measured 0.67 ms per layer, later
-windows 0.59-0.60 ms), so the headline pass that follows, W warmup steps and
-then exactly K timed steps, is measured at the settled clock.
+Pass order: at least 100 untimed layer forwards, then the per-op pass (at
+least 60 forwards), then the headline pass: W warmup steps and exactly K timed
+steps.  The GPU's clocks take a few tens of milliseconds of load to settle
+after idling (the first 20 forwards after 5 warmup steps measured 0.67 ms per
+layer, later windows 0.59-0.60 ms), so both timed passes run at the settled
+clock.
 
 Usage: python bench.py [--steps K] [--warmup W] [--gpus 1]
                        [--workload l64x8|xl_skew|xl128|decode_t{1,8,64,256}|xl128_train|l64x8_train|xl_skew_train]
@@ -562,12 +563,13 @@ def main():
         layer, x = make_layer(hrm, dev, t, h, e, i, k, bias, seed=1234 + c)
         layers.append(layer)
         xs.append(x)
-    # per-op pass first (HIP events around every op, on the op's stream); it also brings the
-    # clocks to their loaded state before the headline pass
+    # untimed forwards first, to bring the clocks to their loaded state; then the per-op pass
+    # (HIP events around every op, on the op's stream), then the headline pass
     from hrm_moe_amd import _lib
 
+    time_layers(layers, xs, max(args.steps, 100), 0)
     timer = OpTimer(hrm.ops)
-    ms_instr, _ = time_layers(layers, xs, max(args.steps, 100), 2, timer)
+    ms_instr, _ = time_layers(layers, xs, max(args.steps, 60), 2, timer)
     timer.restore()
     gate_up_kernel = _lib.last_gemm_kernel(_lib.GEMM_KIND_GATE_UP)
     ms, wall = time_layers(layers, xs, args.steps, args.warmup)
