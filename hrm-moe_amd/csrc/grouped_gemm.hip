@@ -2178,9 +2178,13 @@ int dispatch_mgemm_t(const void* A, const int32_t* gather, const void* W, const 
   MCfg c = mgemm_cfg(M, E, KIND == KIND_GATHER_SWIGLU ? 2 * (int64_t)N : (int64_t)N, KIND == KIND_GATHER_SWIGLU,
                      KIND == KIND_NN);
   if (K % c.bk != 0) c = MCfg{128, 128, 2, 4, 64};
-  // the ring may run at most one tile ahead: STAGES - 1 <= K / BK
+  // the ring may run at most one tile ahead: STAGES - 1 <= K / BK.  The
+  // 32-row tiles are built with 4 or 5 stages only, so short K (the down
+  // projection of experts narrower than 256, or gate/up below a hidden size of
+  // 192) takes the 2-stage 128 x 128 tile.
   if (c.stages - 1 > K / c.bk) {
-    if (c.bk == 32) c = MCfg{c.bm, c.bn, 2, c.waves, 64};
+    if (c.bm == 32) c = MCfg{128, 128, 2, 4, 64};
+    else if (c.bk == 32) c = MCfg{c.bm, c.bn, 2, c.waves, 64};
     else c.stages = 2;
   }
 #define HRM_MG(BM_, BN_, ST_, NW_, BK_) \

@@ -396,9 +396,11 @@ int launch_router_np2(const void* logits, int ldt, int64_t T, int E, int k, int 
 //   dv_j = g_w[j] / c - (sum_i g_w[i] v_i) / c^2 * [s >= 1e-12]   (norm_topk_prob; else dv_j = g_w[j])
 //   dp_e = g_probs[e] + sum_{j: idx_j = e} dv_j                   (topk backward scatters to the chosen experts)
 //   dlogits_e = p_e * (dp_e - sum_e' p_e' dp_e')                  (softmax backward)
-// One wave per token; lane l holds experts l and l + 64.  The two sums over a
-// row are fixed xor butterflies, so results are deterministic.
+// One wave per token; lane l holds experts l + 64 h, h < NE (NE = 2 up to 128
+// experts).  The two sums over a row are fixed xor butterflies, so results
+// are deterministic.
 constexpr int kBwdTokPerBlock = 4;
+template <int NE>
 __global__ __launch_bounds__(kBwdTokPerBlock * 64) void router_bwd_kernel(
     const float* __restrict__ probs, const int64_t* __restrict__ idx, const void* __restrict__ g_w, int gw_dt,
     const float* __restrict__ g_probs, int64_t gp_stride, int64_t T, int E, int k, int norm, void* __restrict__ dlogits,
@@ -426,9 +428,9 @@ __global__ __launch_bounds__(kBwdTokPerBlock * 64) void router_bwd_kernel(
     const float c = fmaxf(sum, 1e-12f);
     dv = gj / c - (sum >= 1e-12f ? dot / (c * c) : 0.0f);
   }
-  float p[2], dp[2];
+  float p[NE], dp[NE];
 #pragma unroll
-  for (int h = 0; h < 2; ++h) {
+  for (int h = 0; h < NE; ++h) {
     const int e = lane + 64 * h;
     p[h] = e < E ? prow[e] : 0.0f;
     dp[h] = (e < E && g_probs) ? g_probs[t * gp_stride + e] : 0.0f;  // stride 0: one row for all tokens
@@ -437,11 +439,14 @@ __global__ __launch_bounds__(kBwdTokPerBlock * 64) void router_bwd_kernel(
     const int e = __shfl(ej, j, 64);
     const float d = __shfl(dv, j, 64);
 #pragma unroll
-    for (int h = 0; h < 2; ++h) dp[h] += (lane + 64 * h == e) ? d : 0.0f;
+    for (int h = 0; h < NE; ++h) dp[h] += (lane + 64 * h == e) ? d : 0.0f;
   }
-  const float pd = wsum(p[0] * dp[0] + p[1] * dp[1]);
+  float part = p[0] * dp[0];
 #pragma unroll
-  for (int h = 0; h < 2; ++h) {
+  for (int h = 1; h < NE; ++h) part = part + p[h] * dp[h];
+  const float pd = wsum(part);
+#pragma unroll
+  for (int h = 0; h < NE; ++h) {
     const int e = lane + 64 * h;
     if (e < E) store_weight(dlogits, out_dt, t * E + e, p[h] * (dp[h] - pd));
   }
@@ -618,6 +623,126 @@ int launch_router_dispatch_wave(const void* logits, int ldt, int64_t T, int E, i
   return HRM_MOE_OK;
 }
 
+// Rows of 129 to 1024 experts: one wave per token, lane l holding experts
+// l + 64 j, j < NE = next_pow2(E) / 64, which is how torch's warp softmax
+// holds rows of up to 1024 fp32 values (persistent softmax, warp size 64):
+// padding elements are -inf, the row maximum and then the sum are taken per
+// lane in j order (the sum starting from 0) and finished with the xor
+// butterfly at distances 32 ... 1; p = e / sum.  Top-k as in the other
+// kernels: k rounds of a row-wide arg-max in (key desc, index asc) order, then
+// torch's ordering network and weight sum.
+constexpr int kWideTokPerBlock = 4;
+template <int NE, int SLOTS, bool KFIX>
+__global__ __launch_bounds__(kWideTokPerBlock * 64) void router_topk_wide_kernel(
+    const void* __restrict__ logits, int ldt, int64_t T, int E, int k_rt, int norm, float* __restrict__ probs,
+    int64_t* __restrict__ idx_out, void* __restrict__ w_out, int wdt) {
+  constexpr int KC = KFIX ? SLOTS : 0;
+  const int k = KFIX ? SLOTS : k_rt;
+  const int lane = threadIdx.x & 63;
+  const int64_t t = (int64_t)blockIdx.x * kWideTokPerBlock + (threadIdx.x >> 6);
+  if (t >= T) return;  // no block barriers below
+  float s[NE];
+  float mx = -INFINITY;
+#pragma unroll
+  for (int j = 0; j < NE; ++j) {
+    const int e = lane + 64 * j;
+    const bool in = e < E;
+    const float f = load_logit(logits, ldt, t * E + (in ? e : 0));
+    s[j] = in ? f : -INFINITY;
+    mx = fmaxf(mx, s[j]);
+  }
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
+  float sum = 0.0f;
+#pragma unroll
+  for (int j = 0; j < NE; ++j) {
+    s[j] = expf(s[j] - mx);
+    sum = sum + s[j];
+  }
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) sum = sum + __shfl_xor(sum, o, 64);
+  uint32_t key[NE];
+#pragma unroll
+  for (int j = 0; j < NE; ++j) {
+    const float p = s[j] / sum;
+    const int e = lane + 64 * j;
+    const bool ok = e < E;
+    if (ok && probs != nullptr) probs[t * E + e] = p;
+    key[j] = ok ? (__float_as_uint(p) + 1u) : 0u;  // 0 marks "not selectable"
+  }
+  uint32_t sk[SLOTS];
+  int si[SLOTS];
+#pragma unroll
+  for (int r = 0; r < SLOTS; ++r) {
+    sk[r] = 0u;
+    si[r] = 0;
+    if (r < k) {
+      uint32_t bk = 0u;
+      int be = 0x7fffffff;
+#pragma unroll
+      for (int j = 0; j < NE; ++j) {
+        const bool b = key[j] > bk;
+        bk = b ? key[j] : bk;
+        be = b ? lane + 64 * j : be;
+      }
+#pragma unroll
+      for (int o = 32; o > 0; o >>= 1) {
+        const uint32_t ok = (uint32_t)__shfl_xor((int)bk, o, 64);
+        const int oe = __shfl_xor(be, o, 64);
+        const bool b = ok > bk || (ok == bk && oe < be);
+        bk = b ? ok : bk;
+        be = b ? oe : be;
+      }
+#pragma unroll
+      for (int j = 0; j < NE; ++j) key[j] = (lane + 64 * j == be) ? 0u : key[j];
+      sk[r] = bk;
+      si[r] = be;
+    }
+  }
+  uint32_t gk[SLOTS];
+  int gi[SLOTS];
+  torch_topk_order<SLOTS, KC>(sk, si, k, gk, gi);
+  float w[SLOTS];
+#pragma unroll
+  for (int j = 0; j < SLOTS; ++j) w[j] = __uint_as_float(gk[j] - 1u);
+  if (norm) {
+    float wsum = torch_row_sum<SLOTS, KC>(w, k);
+    wsum = (wsum != wsum) ? wsum : fmaxf(wsum, 1e-12f);
+#pragma unroll
+    for (int j = 0; j < SLOTS; ++j) w[j] = w[j] / wsum;
+  }
+  int my_i = 0;
+  float my_w = 0.0f;
+#pragma unroll
+  for (int j = 0; j < SLOTS; ++j) {
+    my_i = lane == j ? gi[j] : my_i;
+    my_w = lane == j ? w[j] : my_w;
+  }
+  if (lane < k) {
+    idx_out[t * k + lane] = (int64_t)my_i;
+    store_weight(w_out, wdt, t * k + lane, my_w);
+  }
+}
+
+template <int NE>
+int launch_router_wide(const void* logits, int ldt, int64_t T, int E, int k, int norm, float* probs, int64_t* idx,
+                       void* w, int wdt, void* stream) {
+  const dim3 grid((unsigned)((T + kWideTokPerBlock - 1) / kWideTokPerBlock)), block(kWideTokPerBlock * 64);
+#define HRM_RWD(SL, KF)                                                                                          \
+  HRM_LAUNCH((router_topk_wide_kernel<NE, SL, KF>), grid, block, 0, stream, logits, ldt, T, E, k, norm, probs, idx, \
+             w, wdt)
+  if (k == 2) HRM_RWD(2, true);
+  else if (k == 4) HRM_RWD(4, true);
+  else if (k == 8) HRM_RWD(8, true);
+  else if (k <= 2) HRM_RWD(2, false);
+  else if (k <= 4) HRM_RWD(4, false);
+  else if (k <= 8) HRM_RWD(8, false);
+  else if (k <= 16) HRM_RWD(16, false);
+  else HRM_RWD(32, false);
+#undef HRM_RWD
+  return HRM_MOE_OK;
+}
+
 }  // namespace
 }  // namespace hrm
 
@@ -627,10 +752,18 @@ extern "C" int hrm_moe_router_topk(const void* logits, int logits_dtype, int64_t
   if (num_tokens < 0 || num_experts < 1 || top_k < 1 || top_k > num_experts) return HRM_MOE_ERR_INVALID;
   if (logits_dtype < HRM_MOE_BF16 || logits_dtype > HRM_MOE_F32) return HRM_MOE_ERR_DTYPE;
   if (weight_dtype < HRM_MOE_BF16 || weight_dtype > HRM_MOE_F32) return HRM_MOE_ERR_DTYPE;
-  if (num_experts > 128 || top_k > 32) return HRM_MOE_ERR_UNSUPPORTED;
+  if (num_experts > 1024 || top_k > 32) return HRM_MOE_ERR_UNSUPPORTED;
   if (num_tokens == 0) return HRM_MOE_OK;
   if (!logits || !topk_idx || !topk_weight) return HRM_MOE_ERR_INVALID;
   const int E = num_experts, k = top_k;
+  if (E > 128) {
+#define HRM_WIDE(NE) \
+  hrm::launch_router_wide<NE>(logits, logits_dtype, num_tokens, E, k, norm_topk_prob, probs, topk_idx, topk_weight, weight_dtype, stream)
+    if (E <= 256) return HRM_WIDE(4);
+    if (E <= 512) return HRM_WIDE(8);
+    return HRM_WIDE(16);
+#undef HRM_WIDE
+  }
   if (E <= 8) return hrm::launch_router_np2<8, 4>(logits, logits_dtype, num_tokens, E, k, norm_topk_prob, probs, topk_idx, topk_weight, weight_dtype, stream);
   if (E <= 64) return hrm::launch_router_np2<64, 4>(logits, logits_dtype, num_tokens, E, k, norm_topk_prob, probs, topk_idx, topk_weight, weight_dtype, stream);
   return hrm::launch_router_np2<128, 4>(logits, logits_dtype, num_tokens, E, k, norm_topk_prob, probs, topk_idx, topk_weight, weight_dtype, stream);
@@ -645,14 +778,19 @@ extern "C" int hrm_moe_router_topk_backward(const float* probs, const int64_t* t
   if (grad_probs && grad_probs_row_stride != 0 && grad_probs_row_stride < num_experts) return HRM_MOE_ERR_INVALID;
   if (grad_weight_dtype < HRM_MOE_BF16 || grad_weight_dtype > HRM_MOE_F32) return HRM_MOE_ERR_DTYPE;
   if (logits_dtype < HRM_MOE_BF16 || logits_dtype > HRM_MOE_F32) return HRM_MOE_ERR_DTYPE;
-  if (num_experts > 128 || top_k > 32) return HRM_MOE_ERR_UNSUPPORTED;
+  if (num_experts > 1024 || top_k > 32) return HRM_MOE_ERR_UNSUPPORTED;
   if (num_tokens == 0) return HRM_MOE_OK;
   if (!probs || !topk_idx || !grad_weight || !grad_logits) return HRM_MOE_ERR_INVALID;
   const dim3 grid((unsigned)((num_tokens + hrm::kBwdTokPerBlock - 1) / hrm::kBwdTokPerBlock));
-  hipLaunchKernelGGL(hrm::router_bwd_kernel, grid, dim3(hrm::kBwdTokPerBlock * 64), 0, (hipStream_t)stream, probs,
-                     topk_idx, grad_weight, grad_weight_dtype, grad_probs, grad_probs_row_stride, num_tokens,
-                     num_experts, top_k,
-                     norm_topk_prob, grad_logits, logits_dtype);
+#define HRM_RB(NE)                                                                                                 \
+  hipLaunchKernelGGL(hrm::router_bwd_kernel<NE>, grid, dim3(hrm::kBwdTokPerBlock * 64), 0, (hipStream_t)stream,    \
+                     probs, topk_idx, grad_weight, grad_weight_dtype, grad_probs, grad_probs_row_stride, num_tokens, \
+                     num_experts, top_k, norm_topk_prob, grad_logits, logits_dtype)
+  if (num_experts <= 128) HRM_RB(2);
+  else if (num_experts <= 256) HRM_RB(4);
+  else if (num_experts <= 512) HRM_RB(8);
+  else HRM_RB(16);
+#undef HRM_RB
   const hipError_t err = hipGetLastError();
   return err == hipSuccess ? HRM_MOE_OK : (int)err;
 }

@@ -89,7 +89,8 @@ const char* hrm_moe_last_gemm_kernel(int kind);
  *   probs        [T, E] fp32, may be NULL (needed only for the aux loss)
  *   topk_idx     [T, k] int64
  *   topk_weight  [T, k] in weight_dtype
- * Limits: 1 <= E <= 128, 1 <= k <= min(E, 32).
+ * Limits: 1 <= E <= 1024, 1 <= k <= min(E, 32) (torch's warp softmax, which
+ * the kernels follow, covers rows of up to 1024 fp32 values).
  */
 int hrm_moe_router_topk(const void* logits, int logits_dtype, int64_t num_tokens, int32_t num_experts,
                         int32_t top_k, int32_t norm_topk_prob, float* probs, int64_t* topk_idx,
@@ -283,7 +284,7 @@ int hrm_moe_combine_backward(const void* grad_out, const void* expert_out, const
  * row t at grad_probs + t * grad_probs_row_stride, the stride E for a [T,E]
  * tensor or 0 for one row shared by every token (the auxiliary loss's gradient,
  * which is the same for all tokens).  grad_logits [T,E] in logits_dtype.
- * Deterministic.  Limits: E <= 128, k <= 32. */
+ * Deterministic.  Limits: E <= 1024, k <= 32. */
 int hrm_moe_router_topk_backward(const float* probs, const int64_t* topk_idx, const void* grad_weight,
                                  int grad_weight_dtype, const float* grad_probs, int64_t grad_probs_row_stride,
                                  int64_t num_tokens,

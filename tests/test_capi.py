@@ -54,7 +54,8 @@ def test_router_rejects_bad_arguments():
     call = lambda t, e, k, ldt=0, wdt=0: lib.hrm_moe_router_topk(NULL, ldt, t, e, k, 1, NULL, NULL, NULL, wdt, NULL)
     assert call(4, 0, 1) == _lib.ERR_INVALID
     assert call(4, 8, 9) == _lib.ERR_INVALID
-    assert call(4, 200, 8) == _lib.ERR_UNSUPPORTED
+    assert call(4, 2000, 8) == _lib.ERR_UNSUPPORTED  # up to 1024 experts
+    assert call(4, 200, 8) == _lib.ERR_INVALID  # supported; null tensors
     assert call(4, 64, 33) == _lib.ERR_UNSUPPORTED
     assert call(4, 64, 8, ldt=7) == _lib.ERR_DTYPE
     assert call(0, 64, 8) == _lib.OK  # nothing to do
@@ -124,7 +125,7 @@ def test_training_entry_points_reject_bad_arguments():
     assert rd(buf, 7, 16, 64, 8, 1, buf, buf, buf, _lib.BF16, buf, buf, buf, NULL, buf, buf, rws,
               NULL) == _lib.ERR_DTYPE
     rb = lib.hrm_moe_router_topk_backward
-    assert rb(buf, buf, buf, _lib.BF16, NULL, 0, 16, 200, 8, 1, buf, _lib.BF16, NULL) == _lib.ERR_UNSUPPORTED
+    assert rb(buf, buf, buf, _lib.BF16, NULL, 0, 16, 2000, 8, 1, buf, _lib.BF16, NULL) == _lib.ERR_UNSUPPORTED
     assert rb(buf, buf, buf, 9, NULL, 0, 16, 64, 8, 1, buf, _lib.BF16, NULL) == _lib.ERR_DTYPE
     assert rb(buf, buf, buf, _lib.BF16, NULL, 0, 16, 64, 65, 1, buf, _lib.BF16, NULL) == _lib.ERR_INVALID
     assert rb(buf, NULL, buf, _lib.BF16, NULL, 0, 16, 64, 8, 1, buf, _lib.BF16, NULL) == _lib.ERR_INVALID

@@ -55,6 +55,10 @@ NT_CASES = [
     # decode sizes (32-row tiles): every row in one expert, and a ragged spread
     (512, 1024, 1536, 64, torch.bfloat16, "one"),
     (700, 320, 512, 64, torch.float16, "ragged"),
+    # decode sizes with K below the 32-row tiles' ring depth (they take the 2-stage 128 x 128 tile)
+    (700, 320, 64, 64, torch.bfloat16, "ragged"),
+    (900, 256, 128, 64, torch.bfloat16, "ragged"),
+    (1000, 512, 192, 64, torch.bfloat16, "one"),
 ]
 
 

@@ -55,6 +55,11 @@ LAYER_CASES = [
     ("l_decode_t16", 19, 16, 1280, 64, 448, 8, 0.0),
     # hidden size not a multiple of 64 (register-staged GEMM kernels)
     ("h200", 20, 256, 200, 8, 128, 2, 0.0),
+    # more than 128 experts (wide router, then the separate permute)
+    ("e256", 21, 512, 256, 256, 128, 8, 0.0),
+    ("e1000", 22, 256, 256, 1000, 64, 4, 0.0),
+    # decode size with short K for both GEMMs (H = 128, I = 64)
+    ("h128_decode", 23, 16, 128, 64, 64, 8, 0.0),
 ]
 
 
@@ -184,6 +189,7 @@ def _reference_training_loss(x, wg, wgu, wdn, k, idx, grad):
 @pytest.mark.parametrize("t,h,e,i,k", [
     (512, 256, 8, 128, 2),    # C1 shape in bf16
     (1024, 1280, 64, 448, 8),  # L shape
+    (512, 256, 256, 128, 8),   # more than 128 experts
 ])
 def test_training_path_forward_backward(cuda, t, h, e, i, k):
     layer, (x, wg, wgu, wdn) = build_layer(cuda, 6, t, h, e, i, k)

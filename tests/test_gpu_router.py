@@ -51,6 +51,17 @@ CASES = [
     (1024, 128, 8, torch.bfloat16, torch.bfloat16, True, 0, 6),
     (1024, 8, 2, torch.bfloat16, torch.bfloat16, True, 0, 3),
     (512, 64, 6, torch.bfloat16, torch.bfloat16, True, 0, 5),
+    # more than 128 experts: one wave per token, torch's warp-softmax layout
+    (1024, 256, 8, torch.bfloat16, torch.bfloat16, True, 0.8, 0),
+    (500, 200, 8, torch.bfloat16, torch.bfloat16, True, 1.0, 0),
+    (300, 512, 8, torch.float32, torch.float32, True, 1.0, 0),
+    (257, 1024, 8, torch.bfloat16, torch.bfloat16, True, 1.0, 0),
+    (200, 640, 3, torch.float16, torch.float16, False, 1.0, 0),
+    (128, 384, 16, torch.bfloat16, torch.bfloat16, True, 1.0, 0),
+    (64, 1000, 32, torch.bfloat16, torch.bfloat16, True, 1.0, 0),
+    (512, 256, 8, torch.bfloat16, torch.bfloat16, True, 0, 5),
+    (256, 1024, 8, torch.bfloat16, torch.bfloat16, True, 0, 7),
+    (256, 300, 2, torch.bfloat16, torch.bfloat16, True, 0, 3),
 ]
 
 
@@ -102,6 +113,7 @@ def test_router_zero_tokens(cuda):
 @pytest.mark.parametrize("t,e,k,norm,with_gp", [
     (300, 8, 2, True, True), (1000, 64, 8, True, True), (513, 128, 8, True, False),
     (257, 64, 4, False, True), (64, 16, 16, True, True),
+    (300, 256, 8, True, True), (129, 1024, 8, True, True), (200, 600, 4, False, False),
 ])
 def test_router_backward_matches_oracle(cuda, t, e, k, norm, with_gp):
     """d logits of the router kernel vs CPU autograd of softmax -> gather -> renormalise (oracle.router_vjp)."""
