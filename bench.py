@@ -536,7 +536,7 @@ def main():
     ap.add_argument("--calibrate-copy-mb", type=int, default=0)
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
-        print("bench.py measures one GPU: this build has no multi-GPU path (run with --gpus 1)", file=sys.stderr)
+        print("bench.py measures one GPU: hrm_moe_amd has no multi-GPU path (run with --gpus 1)", file=sys.stderr)
         sys.exit(2)
     assert torch.cuda.is_available(), "bench.py needs a ROCm GPU"
     if args.calibrate_copy_mb:

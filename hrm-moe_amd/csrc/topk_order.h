@@ -1,6 +1,6 @@
 // Ordering of the k selected experts exactly as torch.topk returns them on ROCm.
 //
-// Shared by the router kernel and a host-compiled checker (hostcheck.cpp), so
+// Shared by the router kernel and a host-compiled test library (hostcheck.cpp), so
 // the CPU test suite exercises the same code the kernel runs.
 //
 // torch.topk (sorted) takes every value above the k-th largest in ascending

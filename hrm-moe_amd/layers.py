@@ -249,7 +249,7 @@ class SparseMoEGroupedExperts(nn.Module):
         if num_experts <= 0:
             raise ValueError(f"num_experts must be positive, got {num_experts}")
         if backend not in ("hip", "triton"):
-            raise ValueError(f"Unsupported grouped MoE backend: {backend}; this build provides the HIP kernels only")
+            raise ValueError(f"Unsupported grouped MoE backend: {backend}; hrm_moe_amd provides the HIP kernels only")
         if init_std_in is None:
             init_std_in = 1.0 / (hidden_size ** 0.5)
         if init_std_out is None:
@@ -323,7 +323,7 @@ class SparseMoESwiGLU(nn.Module):
     ``implementation`` accepts "grouped_hip" and, so that existing configs keep
     working, "grouped_triton" (models/layers.py:554-567 with backend triton).
     The reference's other implementations (origin, shard, grouped,
-    grouped_cutlass, grouped_ep) are not part of this build and raise.
+    grouped_cutlass, grouped_ep) are not part of hrm_moe_amd and raise.
     """
 
     IMPLEMENTATIONS = ("grouped_hip", "grouped_triton")

@@ -2,7 +2,7 @@
 
 TEST INFRASTRUCTURE ONLY.  Only ``tests/``, ``__graft_entry__.smoke()`` and the
 ``cpu_baseline`` leg of ``bench.py`` may import anything under ``oracle/``, and
-only as the checker (or the timed CPU baseline), never as part of the product
+only to check results (or as the timed CPU baseline), never as part of the product
 path.  The product path (``hrm_moe_amd``) never imports this package and fails
 loudly when its HIP library is missing.
 

@@ -1,7 +1,7 @@
 """CPU restatement of HRM-MoE's routed SwiGLU MoE FFN (grouped_triton path).
 
 TEST INFRASTRUCTURE ONLY: imported by tests/, __graft_entry__.smoke() and the
-cpu_baseline leg of bench.py, as the checker or as the timed CPU baseline.
+cpu_baseline leg of bench.py, to check results or as the timed CPU baseline.
 The product path never calls it.
 
 Every function names the reference lines it follows (paths relative to the
@@ -399,7 +399,7 @@ def moe_forward_eager(x: torch.Tensor, gate_weight: torch.Tensor, gate_up_weight
     dispatch (:311-322), the per-expert F.linear loop of _torch_grouped_linear
     (moe_triton_grouped_gemm.py:55-65) for both projections, then the
     weighted index_add_ (:333-334).  Numerically this is the reference on the
-    CPU (its top-k tie order is the CPU one); it is timed, not used as the checker.
+    CPU (its top-k tie order is the CPU one); it is timed, not used to check results.
     """
     shape = x.shape
     h = x.reshape(-1, x.shape[-1])

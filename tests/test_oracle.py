@@ -1,4 +1,4 @@
-"""Pins the CPU oracle (oracle/moe_oracle.py) before it is trusted as the checker.
+"""Pins the CPU oracle (oracle/moe_oracle.py) before GPU results are checked against it.
 
 Each oracle function is checked against something it does not restate: the
 reference module's own outputs (C1 golden, imported on the CPU), torch.topk
