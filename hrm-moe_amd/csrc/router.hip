@@ -472,18 +472,27 @@ __global__ __launch_bounds__(kBwdTokPerBlock * 64) void router_bwd_kernel(
 //  * weight sum in torch's order, IEEE division.
 //  * dispatch: stable counting sort of the T*k slots by bucket (expert, or E
 //    for an id outside [0, E)) with the rank step's LDS bitmasks.
+//  * RANK (more than 16 tokens): blocks of 16 tokens, each writing its slots'
+//    ranks within their bucket and its bucket counts (the rank step's output);
+//    the scan + scatter launch then finishes the dispatch.
 constexpr int kWaveRouterMaxTokens = 16;
 
-template <int SLOTS, bool KFIX>
+template <int SLOTS, bool KFIX, bool RANK = false>
 __global__ __launch_bounds__(64 * kWaveRouterMaxTokens) void router_dispatch_wave_kernel(
     const void* __restrict__ logits, int ldt, int T, int E, int k_rt, int norm, float* __restrict__ probs,
-    int64_t* __restrict__ idx_out, void* __restrict__ w_out, int wdt, DispatchOut dout) {
+    int64_t* __restrict__ idx_out, void* __restrict__ w_out, int wdt, DispatchOut dout, int32_t* __restrict__ rank_out,
+    int32_t* __restrict__ counts_out) {
   static_assert(SLOTS <= 8, "k <= 8");
   constexpr int KC = KFIX ? SLOTS : 0;
   constexpr int kMaxWords = (kWaveRouterMaxTokens * 8 + 31) / 32;
   const int k = KFIX ? SLOTS : k_rt;
   const int lane = threadIdx.x & 63;
-  const int t = threadIdx.x >> 6;  // this wave's token; the block has T waves
+  const int tl = threadIdx.x >> 6;  // this wave's token within the block
+  // RANK: blocks of 16 tokens, the last one possibly partial (its idle waves
+  // still pass every barrier); otherwise one block of T waves
+  const int t = RANK ? blockIdx.x * kWaveRouterMaxTokens + tl : tl;
+  const int Tb = RANK ? min(kWaveRouterMaxTokens, T - (int)blockIdx.x * kWaveRouterMaxTokens) : T;
+  const bool active = t < T;
   __shared__ uint64_t s_ck[kWaveRouterMaxTokens][64];
   __shared__ uint32_t s_sk[kWaveRouterMaxTokens][SLOTS];
   __shared__ int32_t s_si[kWaveRouterMaxTokens][SLOTS];
@@ -491,7 +500,7 @@ __global__ __launch_bounds__(64 * kWaveRouterMaxTokens) void router_dispatch_wav
   __shared__ uint32_t s_pref[65 * kMaxWords];
   __shared__ int32_t s_off[65];
 
-  const bool ok = lane < E;
+  const bool ok = active && lane < E;
   const float x = ok ? load_logit(logits, ldt, (int64_t)t * E + lane) : -INFINITY;
   float mx = x;
 #pragma unroll
@@ -506,22 +515,22 @@ __global__ __launch_bounds__(64 * kWaveRouterMaxTokens) void router_dispatch_wav
 
   // rank among the wave's 64 unique (key, 63 - lane) pairs
   const uint64_t ck = ((uint64_t)key << 32) | (uint32_t)(63 - lane);
-  s_ck[t][lane] = ck;
+  s_ck[tl][lane] = ck;
   __syncthreads();
   int rank = 0;
 #pragma unroll
-  for (int j = 0; j < 64; ++j) rank += s_ck[t][j] > ck ? 1 : 0;
+  for (int j = 0; j < 64; ++j) rank += s_ck[tl][j] > ck ? 1 : 0;
   if (rank < k) {
-    s_sk[t][rank] = key;
-    s_si[t][rank] = key != 0u ? lane : 0x7fffffff;
+    s_sk[tl][rank] = key;
+    s_si[tl][rank] = key != 0u ? lane : 0x7fffffff;
   }
   __syncthreads();
   uint32_t sk[SLOTS];
   int si[SLOTS];
 #pragma unroll
   for (int r = 0; r < SLOTS; ++r) {
-    sk[r] = r < k ? s_sk[t][r] : 0u;
-    si[r] = r < k ? s_si[t][r] : 0;
+    sk[r] = r < k ? s_sk[tl][r] : 0u;
+    si[r] = r < k ? s_si[tl][r] : 0;
   }
   bool tie = false;
 #pragma unroll
@@ -553,20 +562,21 @@ __global__ __launch_bounds__(64 * kWaveRouterMaxTokens) void router_dispatch_wav
     my_i = lane == j ? gi[j] : my_i;
     my_w = lane == j ? w[j] : my_w;
   }
-  const bool slot = lane < k;
-  const int ls = t * k + lane;  // flat slot index
+  const bool slot = active && lane < k;
+  const int ls = t * k + lane;    // flat slot index
+  const int lb = tl * k + lane;   // slot index within the block
   if (slot) {
     idx_out[ls] = (int64_t)my_i;
     store_weight(w_out, wdt, ls, my_w);
   }
 
-  // dispatch of the block's T*k slots
+  // dispatch of the block's Tb*k slots
   const int nbk = E + 1;
-  const int words = (T * k + 31) / 32;
+  const int words = (Tb * k + 31) / 32;
   for (int i = threadIdx.x; i < nbk * words; i += blockDim.x) s_mask[i] = 0u;
   __syncthreads();
   const int b = (my_i >= 0 && my_i < E) ? my_i : E;
-  if (slot) atomicOr(&s_mask[b * words + (ls >> 5)], 1u << (ls & 31));
+  if (slot) atomicOr(&s_mask[b * words + (lb >> 5)], 1u << (lb & 31));
   __syncthreads();
   for (int c = threadIdx.x; c < nbk; c += blockDim.x) {
     uint32_t run = 0;
@@ -575,8 +585,16 @@ __global__ __launch_bounds__(64 * kWaveRouterMaxTokens) void router_dispatch_wav
       run += __popc(s_mask[c * words + w2]);
     }
     s_off[c] = (int32_t)run;
+    if constexpr (RANK) counts_out[(int64_t)blockIdx.x * nbk + c] = (int32_t)run;
   }
   __syncthreads();
+  if constexpr (RANK) {
+    if (slot) {
+      const uint32_t below = s_mask[b * words + (lb >> 5)] & ((1u << (lb & 31)) - 1u);
+      rank_out[ls] = (int32_t)(s_pref[b * words + (lb >> 5)] + __popc(below));
+    }
+    return;
+  }
   if (threadIdx.x < 64) {  // bucket totals -> exclusive offsets
     int32_t carry = 0;
     for (int c0 = 0; c0 < nbk; c0 += 64) {
@@ -598,21 +616,32 @@ __global__ __launch_bounds__(64 * kWaveRouterMaxTokens) void router_dispatch_wav
   }
   __syncthreads();
   if (slot) {
-    const uint32_t below = s_mask[b * words + (ls >> 5)] & ((1u << (ls & 31)) - 1u);
-    const int32_t dst = s_off[b] + (int32_t)(s_pref[b * words + (ls >> 5)] + __popc(below));
+    const uint32_t below = s_mask[b * words + (lb >> 5)] & ((1u << (lb & 31)) - 1u);
+    const int32_t dst = s_off[b] + (int32_t)(s_pref[b * words + (lb >> 5)] + __popc(below));
     dout.sorted_token_idx[dst] = t;
     if (dout.sort_idx) dout.sort_idx[dst] = ls;
     dout.slot_to_row[ls] = dst;
   }
 }
 
-// T <= 16 tokens, E <= 64, k <= 8: one block of T waves.
+// T <= 16 tokens, E <= 64, k <= 8: one block of T waves.  With rank/counts
+// (more tokens): blocks of 16 waves, the rank step's output for the scan +
+// scatter launch.
 int launch_router_dispatch_wave(const void* logits, int ldt, int64_t T, int E, int k, int norm, float* probs,
-                                int64_t* idx, void* w, int wdt, const DispatchOut& dout, void* stream) {
-  const dim3 grid(1), block((unsigned)(64 * T));
-#define HRM_RW(SL, KF)                                                                                               \
-  HRM_LAUNCH((router_dispatch_wave_kernel<SL, KF>), grid, block, 0, stream, logits, ldt, (int)T, E, k, norm, probs, \
-             idx, w, wdt, dout)
+                                int64_t* idx, void* w, int wdt, const DispatchOut& dout, void* stream,
+                                int32_t* rank = nullptr, int32_t* counts = nullptr) {
+  const bool rk = rank != nullptr;
+  const dim3 grid(rk ? (unsigned)((T + kWaveRouterMaxTokens - 1) / kWaveRouterMaxTokens) : 1u),
+      block((unsigned)(64 * (rk ? kWaveRouterMaxTokens : T)));
+#define HRM_RW(SL, KF)                                                                                              \
+  do {                                                                                                              \
+    if (rk)                                                                                                         \
+      HRM_LAUNCH((router_dispatch_wave_kernel<SL, KF, true>), grid, block, 0, stream, logits, ldt, (int)T, E, k,   \
+                 norm, probs, idx, w, wdt, dout, rank, counts);                                                     \
+    else                                                                                                            \
+      HRM_LAUNCH((router_dispatch_wave_kernel<SL, KF>), grid, block, 0, stream, logits, ldt, (int)T, E, k, norm,   \
+                 probs, idx, w, wdt, dout, rank, counts);                                                           \
+  } while (0)
   if (k == 2) HRM_RW(2, true);
   else if (k == 4) HRM_RW(4, true);
   else if (k == 8) HRM_RW(8, true);
@@ -800,7 +829,18 @@ extern "C" int hrm_moe_router_topk_backward(const float* probs, const int64_t* t
 // followed by hrm_moe_permute on its topk_idx.
 namespace hrm {
 namespace {
-inline int64_t router_dispatch_blocks(int64_t T) { return (T + 63) / 64; }  // 64 rows per router block
+// From 65 up to this many tokens (E <= 64) the one-wave-per-token router runs
+// with the rank step, in blocks of 16 tokens, and the scan + scatter launch
+// follows; decode layer at T = 256 (graph replay) 96.5 -> 94.0 us.  Up to 64
+// tokens the single-block quad kernel finishes the dispatch in one launch in
+// the same time (T = 64: 84.0 us either way); at 8192 tokens and more the wave
+// kernel's per-token instruction count makes it the slower one.
+constexpr int64_t kWaveRankMaxTokens = 256;
+// rank blocks the router + dispatch workspace holds counts for: 16 tokens each
+// up to kWaveRankMaxTokens (the wave kernel's blocks), else 64 (the quad kernel's)
+inline int64_t router_dispatch_blocks(int64_t T) {
+  return T <= kWaveRankMaxTokens ? (T + kWaveRouterMaxTokens - 1) / kWaveRouterMaxTokens : (T + 63) / 64;
+}
 inline size_t router_dispatch_ws(int64_t T, int E, int k) {
   const size_t r = (size_t)T * (size_t)k;
   return ((sizeof(int32_t) * r + 255) & ~size_t(255)) +
@@ -840,7 +880,7 @@ int router_dispatch(const void* logits, int logits_dtype, int64_t num_tokens, in
                     int64_t* sort_idx, int32_t* slot_to_row, void* workspace, void* stream) {
   const int E = num_experts, k = top_k;
   const int64_t R = num_tokens * k;
-  const int nb = (int)router_dispatch_blocks(num_tokens);
+  const int nb = (int)((num_tokens + 63) / 64);  // the quad kernel's rank blocks: 64 tokens
   char* p = static_cast<char*>(workspace);
   int32_t* rank = reinterpret_cast<int32_t*>(p);
   p += (sizeof(int32_t) * (size_t)R + 255) & ~size_t(255);
@@ -854,6 +894,14 @@ int router_dispatch(const void* logits, int logits_dtype, int64_t num_tokens, in
     if (num_tokens <= kWaveRouterMaxTokens && E <= 64 && config().wave_router)
       return launch_router_dispatch_wave(logits, logits_dtype, num_tokens, E, k, norm_topk_prob, probs, topk_idx,
                                          topk_weight, weight_dtype, dout, stream);
+    if (num_tokens > 64 && num_tokens <= kWaveRankMaxTokens && E <= 64 && config().wave_router) {
+      const int st = launch_router_dispatch_wave(logits, logits_dtype, num_tokens, E, k, norm_topk_prob, probs,
+                                                 topk_idx, topk_weight, weight_dtype, dout, stream, rank, counts);
+      if (st) return st;
+      const int nbw = (int)((num_tokens + kWaveRouterMaxTokens - 1) / kWaveRouterMaxTokens);
+      return dispatch_from_ranks(topk_idx, R, E, k, kWaveRouterMaxTokens * k, nbw, rank, counts, tokens_per_expert,
+                                 expert_offsets, sorted_token_idx, sort_idx, slot_to_row, stream);
+    }
     int st;
     if (E <= 8)
       st = launch_router_rank<8>(logits, logits_dtype, num_tokens, E, k, norm_topk_prob, probs, topk_idx,

@@ -112,13 +112,18 @@ def test_router_dispatch_zero_tokens(cuda):
     (16, 64, 8, torch.bfloat16, torch.bfloat16, True, 3), (16, 64, 8, torch.bfloat16, torch.bfloat16, True, 6),
     (9, 64, 5, torch.bfloat16, torch.bfloat16, True, 2), (16, 8, 8, torch.bfloat16, torch.bfloat16, True, 2),
     (12, 64, 2, torch.bfloat16, torch.bfloat16, False, 4), (1, 64, 8, torch.bfloat16, torch.bfloat16, True, 1),
-    # 17..64 tokens: the single-block quad kernel
+    # 17..64 tokens: the single-block quad kernel; 65..256: the wave kernel in blocks of 16 tokens with the
+    # rank step, then scan + scatter (with HRM_MOE_WAVE_ROUTER=0 the quad kernel's blocks of 64)
     (17, 64, 8, torch.bfloat16, torch.bfloat16, True, 0), (64, 64, 8, torch.bfloat16, torch.bfloat16, True, 0),
     (50, 40, 5, torch.float32, torch.float16, True, 0), (64, 64, 8, torch.bfloat16, torch.bfloat16, True, 3),
-    (33, 8, 2, torch.bfloat16, torch.bfloat16, False, 2), (63, 64, 7, torch.bfloat16, torch.float32, True, 5)])
+    (33, 8, 2, torch.bfloat16, torch.bfloat16, False, 2), (63, 64, 7, torch.bfloat16, torch.float32, True, 5),
+    (100, 64, 8, torch.bfloat16, torch.bfloat16, True, 0), (256, 64, 8, torch.bfloat16, torch.bfloat16, True, 4),
+    (255, 48, 3, torch.float16, torch.bfloat16, True, 0), (200, 64, 8, torch.bfloat16, torch.bfloat16, False, 2),
+    (257, 64, 8, torch.bfloat16, torch.bfloat16, True, 0)])
 def test_router_dispatch_decode_sizes(cuda, wave, t, e, k, ldt, wdt, norm, levels):
-    """Up to 64 tokens (the wave-per-token kernel up to 16, the quad kernel in both settings above) give the bits of
-    router_topk followed by permute, ties included; the indices and weights also equal torch's on the device."""
+    """Decode and mid token counts (the wave-per-token kernel up to 16 tokens and from 65 to 256, the quad kernel
+    otherwise and with the knob off) give the bits of router_topk followed by permute, ties included; the indices
+    and weights also equal torch's on the device."""
     rng = np.random.default_rng(1000 * t + 10 * e + k + levels)
     if levels:
         z = rng.integers(0, levels, size=(t, e)).astype(np.float32) * 0.25
