@@ -59,6 +59,9 @@ NT_CASES = [
     (700, 320, 64, 64, torch.bfloat16, "ragged"),
     (900, 256, 128, 64, torch.bfloat16, "ragged"),
     (1000, 512, 192, 64, torch.bfloat16, "one"),
+    # 16 to 48 rows per expert (64-row tiles), and the same with K below their ring depth
+    (2000, 640, 512, 64, torch.bfloat16, "ragged"),
+    (2000, 256, 64, 64, torch.bfloat16, "ragged"),
 ]
 
 

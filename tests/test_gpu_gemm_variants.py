@@ -24,7 +24,7 @@ pytestmark = pytest.mark.gpu
 
 VARIANTS = ["128x128x2x4x64", "128x128x3x4x64", "128x128x4x4x32", "128x128x5x4x32",
             "256x128x2x4x32", "256x128x3x4x32", "256x256x2x8x64", "256x256x4x8x32", "32x256x4x4x64",
-            "32x128x4x4x64", "32x128x5x4x64"]
+            "32x128x4x4x64", "32x128x5x4x64", "64x128x3x4x64", "64x128x5x4x64"]
 
 
 def _ragged(seed, m, e):
