@@ -21,7 +21,7 @@ BF = torch.bfloat16
 # T, E, k, norm: the maximum the array serves, then smaller inputs (quad router,
 # single-block router, one-wave-per-token router)
 CASES = [(32768, 128, 8, True), (4096, 64, 8, True), (700, 64, 8, True), (40, 64, 6, False), (12, 64, 8, True),
-         (2048, 128, 4, True)]
+         (2048, 128, 4, True), (200, 64, 8, True)]
 
 
 def _outputs(dev, t, e, k):
