@@ -1248,11 +1248,38 @@ __global__ __launch_bounds__(NW * 64, NW == 4 ? 2 : 1) void mgemm_dma_kernel(con
         }
       }
     };
-    // Down projection and dgrad only.  The gather + gate/up kernel keeps the
-    // plain loop: its code built through kloop measured 1-2% slower (L
-    // gate_up +3 us, XL128 +14 us, paired launches), even with every row
-    // block valid.
+    // The gather + gate/up kernel takes kloop only for tiles with a row block
+    // past their last row and keeps the plain loop for full tiles: built
+    // through kloop for every tile it measured 1-2% slower (L gate_up +3 us,
+    // XL128 +14 us, paired launches), even with every row block valid.  With
+    // the split: XL128 gate_up 770 -> 755 us, XL-skew 394 -> 389 us, L the
+    // same (paired launches, bit-identical).
+    // this wave's 32-row blocks that hold a row of the tile (wave-uniform)
+    const int vrows = __builtin_amdgcn_readfirstlane(comp_re - comp_rs) - row_base;
+    const int nvb = vrows <= 0 ? 0 : min((vrows + 31) / 32, MBH);
+    auto ragged_kloop = [&]() __attribute__((always_inline)) {
+      using I0 = std::integral_constant<int, 0>;
+      using I1 = std::integral_constant<int, 1>;
+      using I2 = std::integral_constant<int, 2>;
+      using I3 = std::integral_constant<int, 3>;
+      if (nvb >= MBH) {
+        kloop(std::integral_constant<int, MBH>{});
+      } else if constexpr (MBH == 4) {
+        if (nvb == 3) kloop(I3{});
+        else if (nvb == 2) kloop(I2{});
+        else if (nvb == 1) kloop(I1{});
+        else kloop(I0{});
+      } else if constexpr (MBH == 2) {
+        if (nvb == 1) kloop(I1{});
+        else kloop(I0{});
+      } else {
+        kloop(I0{});
+      }
+    };
     if constexpr (H || KIND == KIND_GATHER_SWIGLU) {
+      if (!H && nvb < MBH) {
+        if constexpr (!H) ragged_kloop();
+      } else {
       for (int kt = 0; kt < nk; ++kt) {
         const int gs = g0 + kt;
         wait_stages<PER, STAGES - 2>(min(STAGES - 2, issued - gs - 1));
@@ -1289,27 +1316,9 @@ __global__ __launch_bounds__(NW * 64, NW == 4 ? 2 : 1) void mgemm_dma_kernel(con
           if (s == 0 && due && late) issue_next();
         }
       }
-    } else {
-      // this wave's 32-row blocks that hold a row of the tile (wave-uniform)
-      const int vrows = __builtin_amdgcn_readfirstlane(comp_re - comp_rs) - row_base;
-      const int nvb = vrows <= 0 ? 0 : min((vrows + 31) / 32, MBH);
-      using I0 = std::integral_constant<int, 0>;
-      using I1 = std::integral_constant<int, 1>;
-      using I2 = std::integral_constant<int, 2>;
-      using I3 = std::integral_constant<int, 3>;
-      if (nvb >= MBH) {
-        kloop(std::integral_constant<int, MBH>{});
-      } else if constexpr (MBH == 4) {
-        if (nvb == 3) kloop(I3{});
-        else if (nvb == 2) kloop(I2{});
-        else if (nvb == 1) kloop(I1{});
-        else kloop(I0{});
-      } else if constexpr (MBH == 2) {
-        if (nvb == 1) kloop(I1{});
-        else kloop(I0{});
-      } else {
-        kloop(I0{});
       }
+    } else {
+      ragged_kloop();
     }
 
     // Epilogue, staged through LDS so that every store writes whole row segments.
