@@ -51,6 +51,7 @@ PROTOTYPES = {
     "hrm_moe_grouped_gemm_tn": (_INT, [_P, _P, _P, _I64, _I64, _I64, _I32, _INT, _P, _P, _SZ, _P]),
     "hrm_moe_gate_up_swiglu": (_INT, [_P, _P, _P, _P, _I64, _I64, _I64, _I64, _I32, _INT, _P, _P, _SZ, _P]),
     "hrm_moe_combine": (_INT, [_P, _P, _P, _P, _I64, _I32, _I64, _I32, _INT, _P, _P]),
+    "hrm_moe_down_combine_decode": (_INT, [_P, _P, _P, _P, _P, _P, _I64, _I32, _I64, _I64, _I32, _INT, _P, _P]),
     "hrm_moe_gate_up_swiglu_save": (_INT, [_P, _P, _P, _P, _I64, _I64, _I64, _I64, _I32, _INT, _P, _P, _P, _SZ, _P]),
     "hrm_moe_down_dgrad_swiglu": (_INT, [_P, _P, _P, _P, _I64, _I64, _I64, _I32, _INT, _P, _P, _SZ, _P]),
     "hrm_moe_combine_backward": (_INT, [_P, _P, _P, _P, _P, _I64, _I32, _I64, _I32, _INT, _P, _P, _P]),

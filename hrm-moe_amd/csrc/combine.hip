@@ -294,6 +294,92 @@ void launch_combine(dim3 grid, dim3 block, void* stream, const char* Y, const in
                        E, O);
 }
 
+// Down projection and combine in one launch for one or two tokens (at most
+// 16 routed rows, where the down GEMM only streams each touched expert's
+// weights once).  Workgroup (column pair cb, token t) computes, for each of
+// t's k <= 8 slots, y = round(act[row] . W_dn[e][c]) for columns c0, c0 + 1,
+// then applies the combine's arithmetic: round(y * w) per slot, summed in
+// fp32 in ascending row order and rounded once (combine_kernel's order).
+// Slots whose row lies past the valid rows contribute nothing.  Workgroups
+// never exchange data, so one launch replaces the down GEMM and the combine.
+// The dot products follow the skinny down GEMM (mgemm_skinny_kernel) step for
+// step, so at the sizes that kernel serves the output is bit-identical to the
+// two launches: the 16 weight rows (slot s = row / 2, column c0 + row % 2) are
+// the A operand of v_mfma_f32_16x16x32, the slots' act rows the B operand
+// (lane l: row / column l % 16, k = 8 (l / 16) .. +7), the 4 waves take K
+// quarters of 32-wide chunks in order, and their partial sums are added in
+// wave order.  D[row][s] for slot s's two rows lands in lane 16 (s / 2) + s.
+// Index loads are clamped to valid slots and the operand loads to row 0 /
+// expert 0, so every load is in bounds and issued unconditionally (one round
+// trip for the indices, one for the operands); dead slots are zeroed after.
+template <typename TR>
+__global__ __launch_bounds__(256) void down_combine_decode_kernel(
+    const uint16_t* __restrict__ act, const uint16_t* __restrict__ W, const int32_t* __restrict__ slot_to_row,
+    const int64_t* __restrict__ topk_idx, const uint16_t* __restrict__ wts, const int32_t* __restrict__ expert_offsets,
+    int k, int H, int I, int E, uint16_t* __restrict__ out) {
+  __shared__ floatx4 red[4][64];
+  __shared__ int32_t s_row[8];
+  __shared__ float s_p[8][2];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int t = blockIdx.y;
+  const int c0 = blockIdx.x * 2;
+  const int64_t tk = (int64_t)t * k;
+  const int32_t r_valid = expert_offsets[E];
+  // B operand: column l % 16 = slot sb's act row; A operand: weight row
+  // l % 16 = slot sa's column c0 + l % 2 (the three index loads go out together)
+  const int sb = lane & 15;
+  const int sa = (lane & 15) >> 1;
+  const int32_t rb = slot_to_row[tk + (sb < k ? sb : k - 1)];
+  const int32_t ra = slot_to_row[tk + (sa < k ? sa : k - 1)];
+  const int64_t ea = topk_idx[tk + (sa < k ? sa : k - 1)];
+  const bool live_b = sb < k && rb >= 0 && rb < r_valid;
+  const bool live_a = sa < k && ra >= 0 && ra < r_valid && ea >= 0 && ea < E;
+  const uint16_t* wa = W + ((int64_t)(live_a ? ea : 0) * H + c0 + (lane & 1)) * I + (lane >> 4) * 8;
+  const uint16_t* xb = act + (int64_t)(live_b ? rb : 0) * I + (lane >> 4) * 8;
+  const int nc = I / 32;
+  const int kc0 = wave * nc / 4, kc1 = (wave + 1) * nc / 4;
+  // chunks past the wave's range (or all four, when I < 128 leaves it none)
+  // reload a valid one and skip its MFMA: no branch separates the index loads
+  // from the operand loads
+  const int kc_hi = kc1 > kc0 ? kc1 - 1 : kc0;
+  u32x4 a[4], b[4];
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    const int kk = (kc0 + u < kc_hi ? kc0 + u : kc_hi) * 32;
+    a[u] = ld16(wa + kk);
+    b[u] = ld16(xb + kk);
+  }
+  const u32x4 zero = u32x4{0u, 0u, 0u, 0u};
+  floatx4 acc = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int u = 0; u < 4; ++u)
+    if (kc0 + u < kc1) acc = TR::mfma16(live_a ? a[u] : zero, live_b ? b[u] : zero, acc);
+  red[wave][lane] = acc;
+  if (wave == 0 && lane < 8) s_row[lane] = live_b ? rb : 0x7fffffff;  // lane < 8: sb = lane
+  __syncthreads();
+  // slot sb's columns c0, c0 + 1 are D rows 2 sb, 2 sb + 1: lane 16 (sb / 2) + sb, v = 2 (sb % 2) + 0, 1
+  if (wave == 0 && sb == 2 * (lane >> 4) + (sb & 1) && live_b) {
+    floatx4 g = red[0][lane];
+#pragma unroll
+    for (int w = 1; w < 4; ++w) g += red[w][lane];
+    int rank = 0;
+    for (int v = 0; v < k; ++v) rank += s_row[v] < rb ? 1 : 0;
+    const float w = TR::to_f(wts[tk + sb]);
+    const int v0 = 2 * (sb & 1);
+    s_p[rank][0] = TR::to_f(TR::from_f(TR::to_f(TR::from_f(g[v0])) * w));
+    s_p[rank][1] = TR::to_f(TR::from_f(TR::to_f(TR::from_f(g[v0 + 1])) * w));
+  }
+  __syncthreads();
+  if (threadIdx.x < 2) {
+    int n_live = 0;
+    for (int v = 0; v < k; ++v) n_live += s_row[v] != 0x7fffffff ? 1 : 0;
+    float o = 0.0f;
+    for (int r = 0; r < n_live; ++r) o += s_p[r][threadIdx.x];
+    out[(int64_t)t * H + c0 + threadIdx.x] = TR::from_f(o);
+  }
+}
+
 }  // namespace
 }  // namespace hrm
 
@@ -363,5 +449,29 @@ extern "C" int hrm_moe_combine_backward(const void* grad_out, const void* expert
                                          hidden_size, num_experts, DY, grad_weight);
   const hipError_t err = hipGetLastError();
   if (err != hipSuccess) return (int)err;
+  return HRM_MOE_OK;
+}
+
+extern "C" int hrm_moe_down_combine_decode(const void* act, const void* down_weight, const int32_t* slot_to_row,
+                                           const int64_t* topk_idx, const void* topk_weight,
+                                           const int32_t* expert_offsets, int64_t num_tokens, int32_t top_k,
+                                           int64_t hidden_size, int64_t inter_size, int32_t num_experts, int dtype,
+                                           void* out, void* stream) {
+  if (num_tokens < 0 || top_k < 1 || hidden_size < 1 || inter_size < 1 || num_experts < 1) return HRM_MOE_ERR_INVALID;
+  if (dtype != HRM_MOE_BF16 && dtype != HRM_MOE_F16) return HRM_MOE_ERR_DTYPE;
+  if (num_tokens > 2 || top_k > 8 || hidden_size % 2 || inter_size % 32 || inter_size > 512 ||
+      hidden_size > (int64_t(1) << 24))
+    return HRM_MOE_ERR_UNSUPPORTED;
+  if (num_tokens == 0) return HRM_MOE_OK;
+  if (!act || !down_weight || !slot_to_row || !topk_idx || !topk_weight || !expert_offsets || !out)
+    return HRM_MOE_ERR_INVALID;
+  const dim3 grid((unsigned)(hidden_size / 2), (unsigned)num_tokens), block(256);
+#define HRM_DC(TR_)                                                                                                  \
+  HRM_LAUNCH(hrm::down_combine_decode_kernel<TR_>, grid, block, 0, stream, (const uint16_t*)act,                     \
+             (const uint16_t*)down_weight, slot_to_row, topk_idx, (const uint16_t*)topk_weight, expert_offsets, top_k, \
+             (int)hidden_size, (int)inter_size, num_experts, (uint16_t*)out)
+  if (dtype == HRM_MOE_BF16) HRM_DC(hrm::BF16);
+  else HRM_DC(hrm::F16);
+#undef HRM_DC
   return HRM_MOE_OK;
 }

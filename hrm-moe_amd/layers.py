@@ -290,6 +290,11 @@ class SparseMoEGroupedExperts(nn.Module):
                 d = dispatch if dispatch is not None else ops.permute(selected_experts, self.num_experts)
             with record_moe_profile_phase("gate_up_gemm"):
                 act = ops.gate_up_swiglu(hidden_states, d, gate_up_weight)
+            if ops.down_combine_decode_ok(act, down_weight, routing_weights):
+                # one or two tokens: down projection and combine in one launch
+                with record_moe_profile_phase("down_gemm"):
+                    return (ops.down_combine_decode(act, down_weight, d, selected_experts, routing_weights),
+                            d.tokens_per_expert)
             with record_moe_profile_phase("down_gemm"):
                 y = ops.grouped_gemm_nt(act, down_weight, d.tokens_per_expert)
             with record_moe_profile_phase("combine"):

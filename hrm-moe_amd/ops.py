@@ -397,6 +397,41 @@ def combine(expert_out: torch.Tensor, dispatch: Dispatch, topk_weight: Optional[
     return out
 
 
+def down_combine_decode_ok(act: torch.Tensor, down_weight: torch.Tensor, topk_weight: torch.Tensor) -> bool:
+    """Whether down_combine_decode covers this call (its limits in include/hrm_moe.h)."""
+    _, h, i = down_weight.shape
+    t, k = topk_weight.shape
+    return (0 < t <= 2 and k <= 8 and h % 2 == 0 and i % 32 == 0 and i <= 512
+            and act.dtype in (torch.bfloat16, torch.float16) and down_weight.dtype == act.dtype
+            and topk_weight.dtype == act.dtype)
+
+
+def down_combine_decode(act: torch.Tensor, down_weight: torch.Tensor, dispatch: Dispatch, topk_idx: torch.Tensor,
+                        topk_weight: torch.Tensor) -> torch.Tensor:
+    """combine(grouped_gemm_nt(act, down_weight), dispatch, topk_weight) in one launch, for one or two tokens.
+
+    The down projection's dot products are this kernel's own fp32 order (not the GEMM kernels'), then the
+    combine's roundings: [T,H].
+    """
+    dev = _require_cuda(act, down_weight, topk_weight)
+    t, k = topk_weight.shape
+    e, h, i = down_weight.shape
+    if act.shape != (t * k, i):
+        raise ValueError(f"act {tuple(act.shape)} for {t} tokens x top-{k} and expert width {i}")
+    if not (act.dtype == down_weight.dtype == topk_weight.dtype):
+        raise TypeError("down_combine_decode needs one dtype for act, weights and routing weights")
+    act, down_weight, topk_weight = act.contiguous(), down_weight.contiguous(), topk_weight.contiguous()
+    topk_idx = topk_idx.to(torch.int64).contiguous()
+    out = act.new_empty((t, h))
+    with _lib.device_guard(dev):
+        st = _lib.lib().hrm_moe_down_combine_decode(
+            _lib.ptr(act), _lib.ptr(down_weight), _lib.ptr(dispatch.slot_to_row), _lib.ptr(topk_idx),
+            _lib.ptr(topk_weight), _lib.ptr(dispatch.expert_offsets), t, k, h, i, e, _lib.dtype_code(act.dtype),
+            _lib.ptr(out), _lib.stream_of(dev))
+    _lib.check(st, "down_combine_decode")
+    return out
+
+
 # ---------------------------------------------------------------------------
 # Training path: saved gate/up, fused SwiGLU backward, combine backward
 # (the quantities torch autograd computes for models/layers.py:317-334)

@@ -233,6 +233,30 @@ int hrm_moe_combine(const void* expert_out, const int32_t* slot_to_row, const vo
                     int32_t num_experts, int dtype, void* out, void* stream);
 
 /*
+ * Down projection and combine in one launch, for one or two tokens
+ * (models/layers.py:331-334: the down grouped linear, the weighting and the
+ * index_add_).  For each token t and column c:
+ *   out[t,c] = sum over t's slots j in ascending row order of
+ *              round( round(act[row_j] . down_weight[e_j][c]) * topk_weight[t,j] )
+ * with fp32 accumulation and one final rounding (row_j = slot_to_row[t*k+j],
+ * e_j = topk_idx[t*k+j]).  The dot products take the decode-size grouped
+ * GEMM's fp32 order (4 K quarters of 16x16x32 MFMA steps, added in order), so
+ * where hrm_moe_grouped_gemm_nt picks its skinny kernel (T*k <= E/4, H a
+ * multiple of 16) the result equals hrm_moe_grouped_gemm_nt followed by
+ * hrm_moe_combine bit for bit.  Slots whose row is >= expert_offsets[E]
+ * contribute nothing.  At these sizes the down GEMM only streams weights, and
+ * one workgroup per 2 output columns computes the rows it needs and combines
+ * them, so no [T*k, H] intermediate is written and no combine launch follows.
+ *   act [T*k, I] (rows in dispatch order), down_weight [E, H, I],
+ *   topk_weight [T, k] in dtype, out [T, H]; dtype bf16 or f16.
+ * Limits: T <= 2, k <= 8, H even, I a multiple of 32 and <= 512.
+ */
+int hrm_moe_down_combine_decode(const void* act, const void* down_weight, const int32_t* slot_to_row,
+                                const int64_t* topk_idx, const void* topk_weight, const int32_t* expert_offsets,
+                                int64_t num_tokens, int32_t top_k, int64_t hidden_size, int64_t inter_size,
+                                int32_t num_experts, int dtype, void* out, void* stream);
+
+/*
  * Training path.  The reference differentiates the grouped composition of
  * models/layers.py:317-334 with torch autograd; these entry points compute the
  * same quantities with the reference's rounding points.

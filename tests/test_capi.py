@@ -62,6 +62,20 @@ def test_router_rejects_bad_arguments():
     assert call(4, 64, 8) == _lib.ERR_INVALID  # null tensors
 
 
+def test_down_combine_decode_rejects_bad_arguments():
+    lib = _lib.load()
+    f = lib.hrm_moe_down_combine_decode
+    buf = ctypes.c_void_p(1 << 20)  # never dereferenced: every call below returns before launching
+    assert f(buf, buf, buf, buf, buf, buf, 3, 8, 1536, 512, 64, _lib.BF16, buf, NULL) == _lib.ERR_UNSUPPORTED
+    assert f(buf, buf, buf, buf, buf, buf, 1, 9, 1536, 512, 64, _lib.BF16, buf, NULL) == _lib.ERR_UNSUPPORTED
+    assert f(buf, buf, buf, buf, buf, buf, 1, 8, 1536, 1024, 64, _lib.BF16, buf, NULL) == _lib.ERR_UNSUPPORTED
+    assert f(buf, buf, buf, buf, buf, buf, 1, 8, 1536, 496, 64, _lib.BF16, buf, NULL) == _lib.ERR_UNSUPPORTED
+    assert f(buf, buf, buf, buf, buf, buf, 1, 8, 1535, 512, 64, _lib.BF16, buf, NULL) == _lib.ERR_UNSUPPORTED
+    assert f(buf, buf, buf, buf, buf, buf, 1, 8, 1536, 512, 64, _lib.F32, buf, NULL) == _lib.ERR_DTYPE
+    assert f(buf, NULL, buf, buf, buf, buf, 1, 8, 1536, 512, 64, _lib.BF16, buf, NULL) == _lib.ERR_INVALID
+    assert f(buf, buf, buf, buf, buf, buf, 0, 8, 1536, 512, 64, _lib.BF16, buf, NULL) == _lib.OK
+
+
 def test_permute_rejects_bad_arguments():
     lib = _lib.load()
     assert lib.hrm_moe_permute_workspace_size(16, 2048, 2) == 0
