@@ -52,6 +52,9 @@ PROTOTYPES = {
     "hrm_moe_gate_up_swiglu": (_INT, [_P, _P, _P, _P, _I64, _I64, _I64, _I64, _I32, _INT, _P, _P, _SZ, _P]),
     "hrm_moe_combine": (_INT, [_P, _P, _P, _P, _I64, _I32, _I64, _I32, _INT, _P, _P]),
     "hrm_moe_down_combine_decode": (_INT, [_P, _P, _P, _P, _P, _P, _I64, _I32, _I64, _I64, _I32, _INT, _P, _P]),
+    "hrm_moe_router_gate_up_decode_supported": (_INT, [_I64, _I64, _I64, _I32, _I32]),
+    "hrm_moe_router_gate_up_decode": (_INT, [_P, _INT, _P, _P, _I64, _I64, _I64, _I32, _I32, _I32, _INT, _P, _P, _P,
+                                             _P, _P, _P, _P, _P, _P, _P]),
     "hrm_moe_gate_up_swiglu_save": (_INT, [_P, _P, _P, _P, _I64, _I64, _I64, _I64, _I32, _INT, _P, _P, _P, _SZ, _P]),
     "hrm_moe_down_dgrad_swiglu": (_INT, [_P, _P, _P, _P, _I64, _I64, _I64, _I32, _INT, _P, _P, _SZ, _P]),
     "hrm_moe_combine_backward": (_INT, [_P, _P, _P, _P, _P, _I64, _I32, _I64, _I32, _INT, _P, _P, _P]),

@@ -53,6 +53,23 @@ __device__ __forceinline__ u32x4 ld16(const void* p) { return *reinterpret_cast<
 __device__ __forceinline__ void st16(void* p, u32x4 v) { *reinterpret_cast<u32x4*>(p) = v; }
 __device__ __forceinline__ void st8(void* p, u32x2 v) { *reinterpret_cast<u32x2*>(p) = v; }
 
+template <typename TR>
+__device__ __forceinline__ u32x2 pack4(float a, float b, float c, float d) {
+  return u32x2{pack2(TR::from_f(a), TR::from_f(b)), pack2(TR::from_f(c), TR::from_f(d))};
+}
+
+// silu(gate) * up with the reference's rounding points (gate, up, silu and the
+// product each rounded to the element type), using the hardware exp2 and
+// reciprocal; it stays within one rounding of torch's expf / IEEE-divide silu.
+template <typename TR>
+__device__ __forceinline__ float swiglu_fast(float g, float u) {
+  const float gr = TR::to_f(TR::from_f(g));
+  const float ur = TR::to_f(TR::from_f(u));
+  const float e = __builtin_amdgcn_exp2f(-gr * 1.4426950408889634f);
+  const float sl = TR::to_f(TR::from_f(gr * __builtin_amdgcn_rcpf(1.0f + e)));
+  return sl * ur;
+}
+
 inline int ceil_div(int64_t a, int64_t b) { return int((a + b - 1) / b); }
 
 // Tuning knobs of the library, read from the environment on first use and

@@ -1,0 +1,243 @@
+// Router, dispatch and gate/up + SwiGLU of one or two tokens, in one launch.
+//
+// Replaces, for a decode step of one or two tokens, models/layers.py:606-610
+// (softmax router + top-k), :312-322 (dispatch) and :325-329 (gate/up grouped
+// linear + SwiGLU).  At these sizes each of them is a few microseconds of
+// latency, so the router launch costs as much as its work.  Here every
+// workgroup routes the tokens itself (route_token_wave, the code of the
+// decode-size router, so the routing is the same bits) and builds the
+// dispatch in LDS; workgroup 0 also writes the router and dispatch outputs.
+// Workgroup (j, cb) then runs the decode-size grouped GEMM's weight-streaming
+// step (mgemm_skinny_kernel with one 16-row block and every K chunk in
+// flight) for the j-th expert with rows and output columns [16 cb, 16 cb + 16),
+// with the SwiGLU epilogue.  The down projection and the combine follow in
+// one more launch (hrm_moe_down_combine_decode), which reads act after this
+// kernel has ended.
+//
+// Taking the down projection and the combine into this launch as well was
+// measured slower: workgroups that wait for every gate/up result (a counter in
+// memory, the act rows read through coherent loads or after an L2
+// invalidate) took 34-52 us per layer at T = 1 against 19.8 us for the three
+// launches, because each hand-over between workgroups on different XCDs
+// costs several dependent memory round trips.
+#include "common.h"
+#include "route_wave.h"
+
+namespace hrm {
+namespace {
+
+constexpr int kDecMaxTokens = 2;
+constexpr int kDecMaxSlots = kDecMaxTokens * 8;
+
+struct DecodeArgs {
+  const void* logits;         // [T, E] in ldt
+  const uint16_t* x;          // [T, H]
+  const uint16_t* w_gu;       // [E, 2I, H]: gate rows [0, I), up rows [I, 2I)
+  float* probs;               // [T, E] or null
+  int64_t* idx_out;           // [T, k]
+  uint16_t* w_out;            // [T, k]
+  int64_t* tokens_per_expert; // [E]
+  int32_t* expert_offsets;    // [E + 1]
+  int32_t* sorted_token_idx;  // [T k]
+  int64_t* sort_idx;          // [T k] or null
+  int32_t* slot_to_row;       // [T k]
+  uint16_t* act;              // [T k, I], rows in dispatch order
+  int ldt, T, E, k, norm, H, I;
+};
+
+template <typename TR, int SLOTS, int CPW>
+__global__ __launch_bounds__(256) void router_gate_up_decode_kernel(DecodeArgs a) {
+  __shared__ uint64_t s_ck[4][64];
+  __shared__ uint32_t s_sk[4][SLOTS];
+  __shared__ int32_t s_si[4][SLOTS];
+  __shared__ int32_t s_e[kDecMaxSlots];    // slot -> bucket: its expert, or E for an id outside [0, E)
+  __shared__ int32_t s_tok[kDecMaxSlots];  // row -> token
+  __shared__ int32_t s_cnt[65];            // bucket -> rows
+  __shared__ int32_t s_off[65];            // bucket -> first row
+  __shared__ floatx4 red[4 * 2 * 64];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  constexpr int k = SLOTS;
+  const int T = a.T, E = a.E;
+  const bool writer = blockIdx.x == 0;
+
+  // ---- routing: wave w routes token w (waves past T pass the barriers idle)
+  int my_i;
+  float my_w;
+  route_token_wave<SLOTS, true>(a.logits, a.ldt, wave, wave < T, E, k, a.norm, writer ? a.probs : nullptr,
+                                s_ck[wave], s_sk[wave], s_si[wave], my_i, my_w);
+  if (wave < T && lane < k) {
+    const int ls = wave * k + lane;
+    s_e[ls] = (my_i >= 0 && my_i < E) ? my_i : E;
+    if (writer) {
+      a.idx_out[ls] = (int64_t)my_i;
+      a.w_out[ls] = TR::from_f(my_w);
+    }
+  }
+  __syncthreads();
+
+  // ---- dispatch: stable order of the R = T k slots by bucket (as the router's counting sort)
+  const int R = T * k;
+  if (tid < R) {
+    const int b = s_e[tid];
+    int dst = 0;
+    for (int s2 = 0; s2 < R; ++s2) {
+      const int b2 = s_e[s2];
+      dst += (b2 < b || (b2 == b && s2 < tid)) ? 1 : 0;
+    }
+    s_tok[dst] = tid / k;
+    if (writer) {
+      a.sorted_token_idx[dst] = tid / k;
+      if (a.sort_idx) a.sort_idx[dst] = tid;
+      a.slot_to_row[tid] = dst;
+    }
+  }
+  if (tid <= E) {
+    int cnt = 0, before = 0;
+    for (int s2 = 0; s2 < R; ++s2) {
+      cnt += s_e[s2] == tid ? 1 : 0;
+      before += s_e[s2] < tid ? 1 : 0;
+    }
+    s_cnt[tid] = cnt;
+    s_off[tid] = before;
+    if (writer) {
+      if (tid < E) a.tokens_per_expert[tid] = cnt;
+      a.expert_offsets[tid] = before;
+    }
+  }
+  __syncthreads();
+
+  // ---- gate/up: expert j (the j-th with rows, ascending id), columns [c0, c0 + 16)
+  const int cblk = a.I / 16;
+  const int j = blockIdx.x / cblk;
+  const int c0 = (blockIdx.x - j * cblk) * 16;
+  const uint64_t nz = __ballot(lane < E && s_cnt[lane] > 0);
+  if (j < __popcll(nz)) {  // uniform over the workgroup
+    const int my_rank = __popcll(nz & ((1ull << lane) - 1ull));
+    const uint64_t hit = __ballot(((nz >> lane) & 1ull) && my_rank == j);
+    const int e = __ffsll((unsigned long long)hit) - 1;
+    const int rs = s_off[e], re = rs + s_cnt[e];
+    const int N = a.I, K = a.H;
+    const uint16_t* wg = a.w_gu + ((int64_t)e * 2 * N + c0 + (lane & 15)) * K + (lane >> 4) * 8;
+    const uint16_t* wu = wg + (int64_t)N * K;
+    const int nc = K / 32;
+    const int kc0 = wave * nc / 4, kc1 = (wave + 1) * nc / 4;
+    int r = rs + (lane & 15);
+    r = r < re ? r : re - 1;  // rows past the expert repeat a valid one; their columns are never stored
+    const uint16_t* xr = a.x + (int64_t)s_tok[r] * K + (lane >> 4) * 8;
+    floatx4 ag = floatx4{0.f, 0.f, 0.f, 0.f}, au = floatx4{0.f, 0.f, 0.f, 0.f};
+    if (kc1 > kc0) {
+      u32x4 bg[CPW], bu[CPW], bx[CPW];
+#pragma unroll
+      for (int u = 0; u < CPW; ++u) {
+        const int kk = (kc0 + u < kc1 ? kc0 + u : kc1 - 1) * 32;
+        bg[u] = ld16(wg + kk);
+        bu[u] = ld16(wu + kk);
+        bx[u] = ld16(xr + kk);
+      }
+#pragma unroll
+      for (int u = 0; u < CPW; ++u) {
+        if (kc0 + u < kc1) {
+          ag = TR::mfma16(bg[u], bx[u], ag);
+          au = TR::mfma16(bu[u], bx[u], au);
+        }
+      }
+    }
+    red[(wave * 2 + 0) * 64 + lane] = ag;
+    red[(wave * 2 + 1) * 64 + lane] = au;
+    __syncthreads();
+    if (wave == 0) {  // the 4 K quarters in wave order; lane l holds columns c0 + 4 (l/16) + v of row l % 16
+      floatx4 gs = red[lane], us = red[64 + lane];
+#pragma unroll
+      for (int w = 1; w < 4; ++w) {
+        gs += red[(w * 2 + 0) * 64 + lane];
+        us += red[(w * 2 + 1) * 64 + lane];
+      }
+      const int row = rs + (lane & 15);
+      if (row < re) {
+        float o[4];
+#pragma unroll
+        for (int v = 0; v < 4; ++v) o[v] = swiglu_fast<TR>(gs[v], us[v]);
+        st8(a.act + (int64_t)row * N + c0 + (lane >> 4) * 4, pack4<TR>(o[0], o[1], o[2], o[3]));
+      }
+    }
+  }
+}
+
+template <typename TR, int SLOTS>
+int launch_router_gate_up_decode(const DecodeArgs& a, int cpw, dim3 grid, void* stream) {
+  if (cpw == 4) HRM_LAUNCH((router_gate_up_decode_kernel<TR, SLOTS, 4>), grid, dim3(256), 0, stream, a);
+  else if (cpw == 8) HRM_LAUNCH((router_gate_up_decode_kernel<TR, SLOTS, 8>), grid, dim3(256), 0, stream, a);
+  else if (cpw == 12) HRM_LAUNCH((router_gate_up_decode_kernel<TR, SLOTS, 12>), grid, dim3(256), 0, stream, a);
+  else HRM_LAUNCH((router_gate_up_decode_kernel<TR, SLOTS, 16>), grid, dim3(256), 0, stream, a);
+  return HRM_MOE_OK;
+}
+
+}  // namespace
+}  // namespace hrm
+
+extern "C" int hrm_moe_router_gate_up_decode_supported(int64_t num_tokens, int64_t hidden_size, int64_t inter_size,
+                                                       int32_t num_experts, int32_t top_k) {
+  if (num_tokens < 1 || num_tokens > hrm::kDecMaxTokens) return 0;
+  if (top_k != 2 && top_k != 4 && top_k != 8) return 0;
+  if (num_experts < top_k || num_experts > 64 || num_tokens * top_k * 4 > num_experts) return 0;
+  if (hidden_size < 64 || hidden_size % 64 || hidden_size > 2048) return 0;
+  if (inter_size < 16 || inter_size % 16) return 0;
+  return 1;
+}
+
+extern "C" int hrm_moe_router_gate_up_decode(const void* logits, int logits_dtype, const void* hidden,
+                                             const void* gate_up_weight, int64_t num_tokens, int64_t hidden_size,
+                                             int64_t inter_size, int32_t num_experts, int32_t top_k,
+                                             int32_t norm_topk_prob, int dtype, float* probs, int64_t* topk_idx,
+                                             void* topk_weight, int64_t* tokens_per_expert,
+                                             int32_t* expert_offsets, int32_t* sorted_token_idx, int64_t* sort_idx,
+                                             int32_t* slot_to_row, void* act, void* stream) {
+  if (num_tokens < 0 || hidden_size < 1 || inter_size < 1 || num_experts < 1 || top_k < 1 || top_k > num_experts)
+    return HRM_MOE_ERR_INVALID;
+  if (dtype != HRM_MOE_BF16 && dtype != HRM_MOE_F16) return HRM_MOE_ERR_DTYPE;
+  if (logits_dtype < HRM_MOE_BF16 || logits_dtype > HRM_MOE_F32) return HRM_MOE_ERR_DTYPE;
+  if (num_tokens == 0) return HRM_MOE_OK;
+  if (!hrm_moe_router_gate_up_decode_supported(num_tokens, hidden_size, inter_size, num_experts, top_k))
+    return HRM_MOE_ERR_UNSUPPORTED;
+  if (!logits || !hidden || !gate_up_weight || !topk_idx || !topk_weight || !tokens_per_expert || !expert_offsets ||
+      !sorted_token_idx || !slot_to_row || !act)
+    return HRM_MOE_ERR_INVALID;
+  hrm::DecodeArgs a;
+  a.logits = logits;
+  a.x = static_cast<const uint16_t*>(hidden);
+  a.w_gu = static_cast<const uint16_t*>(gate_up_weight);
+  a.probs = probs;
+  a.idx_out = topk_idx;
+  a.w_out = static_cast<uint16_t*>(topk_weight);
+  a.tokens_per_expert = tokens_per_expert;
+  a.expert_offsets = expert_offsets;
+  a.sorted_token_idx = sorted_token_idx;
+  a.sort_idx = sort_idx;
+  a.slot_to_row = slot_to_row;
+  a.act = static_cast<uint16_t*>(act);
+  a.ldt = logits_dtype;
+  a.T = (int)num_tokens;
+  a.E = num_experts;
+  a.k = top_k;
+  a.norm = norm_topk_prob ? 1 : 0;
+  a.H = (int)hidden_size;
+  a.I = (int)inter_size;
+  // one workgroup group per expert that can have rows (at most T k of them), I / 16 column blocks each
+  const int64_t experts_max = num_tokens * top_k < num_experts ? num_tokens * top_k : num_experts;
+  const dim3 grid((unsigned)(experts_max * (inter_size / 16)));
+  // K chunks per wave (4 waves split H in 32-wide chunks), all in flight at once
+  const int need = (int)((hidden_size / 32 + 3) / 4);
+  const int cpw = need <= 4 ? 4 : (need <= 8 ? 8 : (need <= 12 ? 12 : 16));
+#define HRM_RG(TR_)                                                                            \
+  do {                                                                                         \
+    if (top_k == 2) return hrm::launch_router_gate_up_decode<TR_, 2>(a, cpw, grid, stream);    \
+    if (top_k == 4) return hrm::launch_router_gate_up_decode<TR_, 4>(a, cpw, grid, stream);    \
+    return hrm::launch_router_gate_up_decode<TR_, 8>(a, cpw, grid, stream);                    \
+  } while (0)
+  if (dtype == HRM_MOE_BF16) HRM_RG(hrm::BF16);
+  HRM_RG(hrm::F16);
+#undef HRM_RG
+}

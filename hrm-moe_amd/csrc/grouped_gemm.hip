@@ -204,11 +204,6 @@ __device__ __forceinline__ u32x4 tr_operand(const char* base, int col0, int s, i
   return u32x4{lo.x, lo.y, hi.x, hi.y};
 }
 
-template <typename TR>
-__device__ __forceinline__ u32x2 pack4(float a, float b, float c, float d) {
-  return u32x2{pack2(TR::from_f(a), TR::from_f(b)), pack2(TR::from_f(c), TR::from_f(d))};
-}
-
 // silu(gate) * up with the reference's roundings: gate, up, silu(gate) and the
 // product are each rounded to the element type (models/layers.py:328-329 on
 // 16-bit tensors; torch's silu computes x / (1 + exp(-x)) in fp32).
@@ -814,18 +809,6 @@ __device__ __forceinline__ void wait_stages(int ahead) {
     if (ahead >= 1) { wait_vmcnt<PER>(); return; }
   }
   wait_vmcnt<0>();
-}
-
-// silu(gate) * up with the reference's rounding points (gate, up, silu and the
-// product each rounded to the element type), using the hardware exp2 and
-// reciprocal; it stays within one rounding of torch's expf / IEEE-divide silu.
-template <typename TR>
-__device__ __forceinline__ float swiglu_fast(float g, float u) {
-  const float gr = TR::to_f(TR::from_f(g));
-  const float ur = TR::to_f(TR::from_f(u));
-  const float e = __builtin_amdgcn_exp2f(-gr * 1.4426950408889634f);
-  const float sl = TR::to_f(TR::from_f(gr * __builtin_amdgcn_rcpf(1.0f + e)));
-  return sl * ur;
 }
 
 // Backward of silu(g) * u for one element, with the reference's rounding

@@ -29,6 +29,7 @@
 #include <mutex>
 
 #include "common.h"
+#include "route_wave.h"
 #include "topk_order.h"
 
 namespace hrm {
@@ -46,18 +47,6 @@ __device__ __forceinline__ uint32_t xlane(uint32_t x) {
 template <int D>
 __device__ __forceinline__ float xlanef(float x) {
   return __uint_as_float(xlane<D>(__float_as_uint(x)));
-}
-
-__device__ __forceinline__ float load_logit(const void* p, int dt, int64_t i) {
-  if (dt == HRM_MOE_BF16) return BF16::to_f(reinterpret_cast<const uint16_t*>(p)[i]);
-  if (dt == HRM_MOE_F16) return F16::to_f(reinterpret_cast<const uint16_t*>(p)[i]);
-  return reinterpret_cast<const float*>(p)[i];
-}
-
-__device__ __forceinline__ void store_weight(void* p, int dt, int64_t i, float w) {
-  if (dt == HRM_MOE_BF16) reinterpret_cast<uint16_t*>(p)[i] = BF16::from_f(w);
-  else if (dt == HRM_MOE_F16) reinterpret_cast<uint16_t*>(p)[i] = F16::from_f(w);
-  else reinterpret_cast<float*>(p)[i] = w;
 }
 
 // One selection round over the row's lanes: the largest remaining key, ties
@@ -457,7 +446,9 @@ __global__ __launch_bounds__(kBwdTokPerBlock * 64) void router_bwd_kernel(
 // wave of the quad kernel runs the same serial chain (k arg-max rounds over
 // 16 experts per lane, then the ordering network) whether it holds 16 rows or
 // one; here each step is a handful of instructions.  Same arithmetic as
-// router_topk_kernel, so the outputs are the same bits:
+// router_topk_kernel, so the outputs are the same bits.  The per-token part
+// is route_token_wave (route_wave.h), which the one-launch decode layer
+// shares:
 //  * softmax: the xor butterfly over lanes at distances 32 ... 1 is the
 //    pairwise tree S_e <- S_e + S_(e^o) that the quad kernel evaluates
 //    (cross-lane levels, then in-lane levels); fp32 addition commutes, so
@@ -483,7 +474,6 @@ __global__ __launch_bounds__(64 * kWaveRouterMaxTokens) void router_dispatch_wav
     int64_t* __restrict__ idx_out, void* __restrict__ w_out, int wdt, DispatchOut dout, int32_t* __restrict__ rank_out,
     int32_t* __restrict__ counts_out) {
   static_assert(SLOTS <= 8, "k <= 8");
-  constexpr int KC = KFIX ? SLOTS : 0;
   constexpr int kMaxWords = (kWaveRouterMaxTokens * 8 + 31) / 32;
   const int k = KFIX ? SLOTS : k_rt;
   const int lane = threadIdx.x & 63;
@@ -500,68 +490,9 @@ __global__ __launch_bounds__(64 * kWaveRouterMaxTokens) void router_dispatch_wav
   __shared__ uint32_t s_pref[65 * kMaxWords];
   __shared__ int32_t s_off[65];
 
-  const bool ok = active && lane < E;
-  const float x = ok ? load_logit(logits, ldt, (int64_t)t * E + lane) : -INFINITY;
-  float mx = x;
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
-  const float s = expf(x - mx);
-  float total = s;
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) total = total + __shfl_xor(total, o, 64);
-  const float p = s / total;
-  if (ok && probs != nullptr) probs[(int64_t)t * E + lane] = p;
-  const uint32_t key = ok ? (__float_as_uint(p) + 1u) : 0u;  // 0 marks "not selectable"
-
-  // rank among the wave's 64 unique (key, 63 - lane) pairs
-  const uint64_t ck = ((uint64_t)key << 32) | (uint32_t)(63 - lane);
-  s_ck[tl][lane] = ck;
-  __syncthreads();
-  int rank = 0;
-#pragma unroll
-  for (int j = 0; j < 64; ++j) rank += s_ck[tl][j] > ck ? 1 : 0;
-  if (rank < k) {
-    s_sk[tl][rank] = key;
-    s_si[tl][rank] = key != 0u ? lane : 0x7fffffff;
-  }
-  __syncthreads();
-  uint32_t sk[SLOTS];
-  int si[SLOTS];
-#pragma unroll
-  for (int r = 0; r < SLOTS; ++r) {
-    sk[r] = r < k ? s_sk[tl][r] : 0u;
-    si[r] = r < k ? s_si[tl][r] : 0;
-  }
-  bool tie = false;
-#pragma unroll
-  for (int r = 0; r + 1 < SLOTS; ++r) tie = tie || (r + 1 < k && sk[r] == sk[r + 1]);
-  uint32_t gk[SLOTS];
-  int gi[SLOTS];
-  if (__builtin_amdgcn_readfirstlane((int)tie)) {
-    torch_topk_order<SLOTS, KC>(sk, si, k, gk, gi);
-  } else {
-#pragma unroll
-    for (int r = 0; r < SLOTS; ++r) {
-      gk[r] = sk[r];
-      gi[r] = si[r];
-    }
-  }
-  float w[SLOTS];
-#pragma unroll
-  for (int j = 0; j < SLOTS; ++j) w[j] = __uint_as_float(gk[j] - 1u);
-  if (norm) {
-    float sum = torch_row_sum<SLOTS, KC>(w, k);
-    sum = (sum != sum) ? sum : fmaxf(sum, 1e-12f);
-#pragma unroll
-    for (int j = 0; j < SLOTS; ++j) w[j] = w[j] / sum;
-  }
-  int my_i = 0;
-  float my_w = 0.0f;
-#pragma unroll
-  for (int j = 0; j < SLOTS; ++j) {
-    my_i = lane == j ? gi[j] : my_i;
-    my_w = lane == j ? w[j] : my_w;
-  }
+  int my_i;
+  float my_w;
+  route_token_wave<SLOTS, KFIX>(logits, ldt, t, active, E, k, norm, probs, s_ck[tl], s_sk[tl], s_si[tl], my_i, my_w);
   const bool slot = active && lane < k;
   const int ls = t * k + lane;    // flat slot index
   const int lb = tl * k + lane;   // slot index within the block

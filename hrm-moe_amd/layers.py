@@ -10,7 +10,10 @@ Forward paths (same arithmetic, same routing bits):
     grad): router kernel -> dispatch kernel -> fused gather + gate_up GEMM +
     SwiGLU -> down GEMM -> deterministic combine.  Five HIP launches plus the
     gate GEMM; no host synchronisation.  Any hidden size that is a multiple
-    of 8.
+    of 8.  A decode step of one or two tokens (within the limits of
+    ops.router_gate_up_decode_ok and ops.down_combine_decode_ok) runs the
+    router, dispatch and gate_up in one launch and the down GEMM and combine
+    in a second, with the same bits.
   * autograd needed: the same forward kernels (the gate/up kernel also saving
     the rounded gate/up values) inside one autograd function whose backward
     is HIP too: combine backward, down dgrad with the SwiGLU backward fused,
@@ -366,6 +369,7 @@ class SparseMoESwiGLU(nn.Module):
         want_aux = moe_context is not None and torch.is_grad_enabled()
 
         dispatch = None
+        decoded = None
         with record_moe_profile_phase("router"):
             w_gate = self.gate.weight
             if (torch.is_grad_enabled() and w_gate.requires_grad and self.gate.bias is None
@@ -381,15 +385,22 @@ class SparseMoESwiGLU(nn.Module):
                 dispatch = ops.Dispatch(*dd, None)
             elif self.num_experts <= 128 and self.top_k <= 8 and not self.experts._needs_autograd(
                     hidden_states, router_logits):
-                # router and dispatch in two launches
-                routing_probs, routing_weights, selected_experts, dispatch = ops.router_topk_dispatch(
-                    router_logits, self.top_k, self.norm_topk_prob, hidden_states.dtype, want_probs=want_aux)
+                decoded = self._decode_two_launches(hidden_states, router_logits, want_aux)
+                if decoded is not None:
+                    routing_probs, routing_weights, selected_experts, dispatch, final_hidden_states = decoded
+                else:
+                    # router and dispatch in two launches
+                    routing_probs, routing_weights, selected_experts, dispatch = ops.router_topk_dispatch(
+                        router_logits, self.top_k, self.norm_topk_prob, hidden_states.dtype, want_probs=want_aux)
             else:
                 routing_probs, routing_weights, selected_experts = ops.router_topk(
                     router_logits, self.top_k, self.norm_topk_prob, hidden_states.dtype, want_probs=want_aux)
 
-        final_hidden_states, tokens_per_expert = self.experts._compute(hidden_states, selected_experts,
-                                                                       routing_weights, dispatch)
+        if decoded is not None:
+            tokens_per_expert = dispatch.tokens_per_expert
+        else:
+            final_hidden_states, tokens_per_expert = self.experts._compute(hidden_states, selected_experts,
+                                                                           routing_weights, dispatch)
 
         if want_aux:
             aux_routing_probs = routing_probs
@@ -417,3 +428,23 @@ class SparseMoESwiGLU(nn.Module):
                         moe_context.setdefault("expert_counts", []).append(counts.to(torch.float32))
 
         return final_hidden_states.reshape(original_shape)
+
+    def _decode_two_launches(self, hidden_states: Tensor, router_logits: Tensor, want_probs: bool):
+        """(probs, weights, idx, Dispatch, expert output) of one or two tokens: router, dispatch and gate_up in one
+        launch, then the down GEMM and combine; None when the call is outside the first launch's limits."""
+        if hidden_states.shape[0] > 2 or not hidden_states.is_cuda:
+            return None
+        dtype = hidden_states.dtype
+        gate_up_weight = self.experts.gate_up_weight.to(dtype)
+        if not ops.router_gate_up_decode_ok(router_logits, hidden_states, gate_up_weight, self.top_k):
+            return None
+        down_weight = self.experts.down_weight.to(dtype)
+        with record_moe_profile_phase("router_gate_up"):
+            probs, w, idx, d, act = ops.router_gate_up_decode(router_logits, hidden_states, gate_up_weight,
+                                                               self.top_k, self.norm_topk_prob, want_probs=want_probs)
+        with record_moe_profile_phase("down_gemm"):
+            if ops.down_combine_decode_ok(act, down_weight, w):
+                return probs, w, idx, d, ops.down_combine_decode(act, down_weight, d, idx, w)
+            y = ops.grouped_gemm_nt(act, down_weight, d.tokens_per_expert)
+        with record_moe_profile_phase("combine"):
+            return probs, w, idx, d, ops.combine(y, d, w)

@@ -432,6 +432,52 @@ def down_combine_decode(act: torch.Tensor, down_weight: torch.Tensor, dispatch: 
     return out
 
 
+def router_gate_up_decode_ok(logits: torch.Tensor, hidden: torch.Tensor, gate_up_weight: torch.Tensor,
+                             top_k: int) -> bool:
+    """Whether router_gate_up_decode covers this call (its limits in include/hrm_moe.h)."""
+    if hidden.dim() != 2 or logits.dim() != 2 or gate_up_weight.dim() != 3:
+        return False
+    t, h = hidden.shape
+    e, i2, h2 = gate_up_weight.shape
+    return (hidden.dtype in (torch.bfloat16, torch.float16) and gate_up_weight.dtype == hidden.dtype
+            and logits.dtype in _lib.DTYPE_CODE and h2 == h and i2 % 2 == 0 and tuple(logits.shape) == (t, e)
+            and bool(_lib.lib().hrm_moe_router_gate_up_decode_supported(t, h, i2 // 2, e, top_k)))
+
+
+def router_gate_up_decode(logits: torch.Tensor, hidden: torch.Tensor, gate_up_weight: torch.Tensor, top_k: int,
+                          norm_topk_prob: bool, want_probs: bool = False, want_sort_idx: bool = False):
+    """router_topk_dispatch then gate_up_swiglu, in one launch, for one or two tokens.
+
+    Returns (probs or None, weights [T,k], idx [T,k], Dispatch, act [T*k, I]), the same bits as the two ops;
+    down_combine_decode finishes the layer.
+    """
+    dev = _require_cuda(logits, hidden, gate_up_weight)
+    if not router_gate_up_decode_ok(logits, hidden, gate_up_weight, top_k):
+        raise ValueError("router_gate_up_decode does not cover this call (see router_gate_up_decode_ok)")
+    logits, hidden, gate_up_weight = logits.contiguous(), hidden.contiguous(), gate_up_weight.contiguous()
+    t, h = hidden.shape
+    e, i2, _ = gate_up_weight.shape
+    i = i2 // 2
+    r = t * top_k
+    probs = torch.empty((t, e), dtype=torch.float32, device=dev) if want_probs else None
+    idx = torch.empty((t, top_k), dtype=torch.int64, device=dev)
+    w = torch.empty((t, top_k), dtype=hidden.dtype, device=dev)
+    tpe = torch.empty(e, dtype=torch.int64, device=dev)
+    offsets = torch.empty(e + 1, dtype=torch.int32, device=dev)
+    sorted_token_idx = torch.empty(r, dtype=torch.int32, device=dev)
+    slot_to_row = torch.empty(r, dtype=torch.int32, device=dev)
+    sort_idx = torch.empty(r, dtype=torch.int64, device=dev) if want_sort_idx else None
+    act = hidden.new_empty((r, i))
+    with _lib.device_guard(dev):
+        st = _lib.lib().hrm_moe_router_gate_up_decode(
+            _lib.ptr(logits), _lib.dtype_code(logits.dtype), _lib.ptr(hidden), _lib.ptr(gate_up_weight), t, h, i, e,
+            top_k, int(bool(norm_topk_prob)), _lib.dtype_code(hidden.dtype), _lib.ptr(probs), _lib.ptr(idx),
+            _lib.ptr(w), _lib.ptr(tpe), _lib.ptr(offsets), _lib.ptr(sorted_token_idx), _lib.ptr(sort_idx),
+            _lib.ptr(slot_to_row), _lib.ptr(act), _lib.stream_of(dev))
+    _lib.check(st, "router_gate_up_decode")
+    return probs, w, idx, Dispatch(tpe, offsets, sorted_token_idx, slot_to_row, sort_idx), act
+
+
 # ---------------------------------------------------------------------------
 # Training path: saved gate/up, fused SwiGLU backward, combine backward
 # (the quantities torch autograd computes for models/layers.py:317-334)

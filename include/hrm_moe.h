@@ -257,6 +257,33 @@ int hrm_moe_down_combine_decode(const void* act, const void* down_weight, const 
                                 int32_t num_experts, int dtype, void* out, void* stream);
 
 /*
+ * Router, dispatch and gate/up grouped linear + SwiGLU in one launch, for one
+ * or two tokens (models/layers.py:606-610, :312-322 and :325-329 of a decode
+ * step).  Its outputs are the bits of hrm_moe_router_topk_dispatch followed by
+ * hrm_moe_gate_up_swiglu on the same inputs (routing, probabilities, the
+ * dispatch tensors and act), where hrm_moe_router_gate_up_decode_supported
+ * says the call is covered: at these sizes the router launch costs as much as
+ * its work.  hrm_moe_down_combine_decode then finishes the layer.
+ *   logits [T,E] (logits_dtype), hidden [T,H], gate_up_weight [E,2I,H];
+ *   outputs probs [T,E] fp32 (may be NULL), topk_idx [T,k] int64, topk_weight
+ *   [T,k] in dtype, tokens_per_expert [E] int64, expert_offsets [E+1],
+ *   sorted_token_idx [T*k], sort_idx [T*k] int64 (may be NULL), slot_to_row
+ *   [T*k], act [T*k, I] (the SwiGLU rows in dispatch order); dtype bf16 or
+ *   f16 for hidden, weights, topk_weight and act.
+ * Limits (hrm_moe_router_gate_up_decode_supported): 1 <= T <= 2, k in
+ * {2, 4, 8}, 4*T*k <= E <= 64, H a multiple of 64 and <= 2048, I a multiple
+ * of 16.
+ */
+int hrm_moe_router_gate_up_decode_supported(int64_t num_tokens, int64_t hidden_size, int64_t inter_size,
+                                            int32_t num_experts, int32_t top_k);
+int hrm_moe_router_gate_up_decode(const void* logits, int logits_dtype, const void* hidden,
+                                  const void* gate_up_weight, int64_t num_tokens, int64_t hidden_size,
+                                  int64_t inter_size, int32_t num_experts, int32_t top_k, int32_t norm_topk_prob,
+                                  int dtype, float* probs, int64_t* topk_idx, void* topk_weight,
+                                  int64_t* tokens_per_expert, int32_t* expert_offsets, int32_t* sorted_token_idx,
+                                  int64_t* sort_idx, int32_t* slot_to_row, void* act, void* stream);
+
+/*
  * Training path.  The reference differentiates the grouped composition of
  * models/layers.py:317-334 with torch autograd; these entry points compute the
  * same quantities with the reference's rounding points.

@@ -76,6 +76,30 @@ def test_down_combine_decode_rejects_bad_arguments():
     assert f(buf, buf, buf, buf, buf, buf, 0, 8, 1536, 512, 64, _lib.BF16, buf, NULL) == _lib.OK
 
 
+def test_router_gate_up_decode_limits_and_bad_arguments():
+    lib = _lib.load()
+    ok = lib.hrm_moe_router_gate_up_decode_supported
+    assert ok(1, 1536, 512, 64, 8) == 1 and ok(2, 1536, 512, 64, 8) == 1
+    assert ok(3, 1536, 512, 64, 8) == 0          # more than two tokens
+    assert ok(1, 1536, 512, 64, 6) == 0          # k outside {2, 4, 8}
+    assert ok(2, 1536, 512, 32, 8) == 0          # 4 T k > E: the grouped GEMM would not only stream weights
+    assert ok(1, 1536, 512, 128, 8) == 0         # one wave routes a token: E <= 64
+    assert ok(1, 1504, 512, 64, 8) == 0          # H not a multiple of 64
+    assert ok(1, 4096, 512, 64, 8) == 0          # H above 2048
+    assert ok(1, 1536, 504, 64, 8) == 0          # I not a multiple of 16
+    f = lib.hrm_moe_router_gate_up_decode
+    buf = ctypes.c_void_p(1 << 20)  # never dereferenced: every call below returns before launching
+    args = lambda t=1, h=1536, i=512, e=64, k=8, dt=_lib.BF16, ldt=_lib.BF16, act=buf: (
+        buf, ldt, buf, buf, t, h, i, e, k, 1, dt, NULL, buf, buf, buf, buf, buf, NULL, buf, act, NULL)
+    assert f(*args(t=3)) == _lib.ERR_UNSUPPORTED
+    assert f(*args(k=6)) == _lib.ERR_UNSUPPORTED
+    assert f(*args(k=65)) == _lib.ERR_INVALID
+    assert f(*args(dt=_lib.F32)) == _lib.ERR_DTYPE
+    assert f(*args(ldt=7)) == _lib.ERR_DTYPE
+    assert f(*args(act=NULL)) == _lib.ERR_INVALID
+    assert f(*args(t=0)) == _lib.OK
+
+
 def test_permute_rejects_bad_arguments():
     lib = _lib.load()
     assert lib.hrm_moe_permute_workspace_size(16, 2048, 2) == 0
