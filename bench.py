@@ -261,7 +261,9 @@ def cpu_baseline(t, h, e, i, k, bias_std=0.0, runs=5, legs=()):
 
 
 def decode_gate_up_us(layers, xs, dispatches, reps):
-    """Average duration (us) of the gate_up kernel alone at a decode size, and its instantiation.
+    """Average duration (us) of the layer's gate_up kernel alone at a decode size, its instantiation, and
+    whether it is the one-launch router + dispatch + gate_up kernel (one or two tokens) rather than the
+    gate_up GEMM after the router.
 
     One HIP graph holds one launch per weight copy, back to back; HIP events on
     the replaying stream bracket ``reps`` replays.
@@ -269,17 +271,26 @@ def decode_gate_up_us(layers, xs, dispatches, reps):
     from hrm_moe_amd import _lib, ops
 
     weights = [layer.experts.gate_up_weight.to(x.dtype) for layer, x in zip(layers, xs)]
+    k = layers[0].top_k
     with torch.no_grad():
+        logits = [torch.nn.functional.linear(x, layer.gate.weight) for layer, x in zip(layers, xs)]
+        fused = ops.router_gate_up_decode_ok(logits[0], xs[0], weights[0], k)
+
+        def body():
+            for c, (x, d, w) in enumerate(zip(xs, dispatches, weights)):
+                if fused:
+                    ops.router_gate_up_decode(logits[c], x, w, k, True)
+                else:
+                    ops.gate_up_swiglu(x, d, w)
+
         side = torch.cuda.Stream()  # default priority
         side.wait_stream(torch.cuda.current_stream())
         with torch.cuda.stream(side):
-            for x, d, w in zip(xs, dispatches, weights):
-                ops.gate_up_swiglu(x, d, w)
+            body()
         torch.cuda.current_stream().wait_stream(side)
         graph = torch.cuda.CUDAGraph()
         with torch.cuda.graph(graph):
-            for x, d, w in zip(xs, dispatches, weights):
-                ops.gate_up_swiglu(x, d, w)
+            body()
     kernel = _lib.last_gemm_kernel(_lib.GEMM_KIND_GATE_UP)
     for _ in range(3):
         graph.replay()
@@ -291,7 +302,7 @@ def decode_gate_up_us(layers, xs, dispatches, reps):
         graph.replay()
     end.record()
     torch.cuda.synchronize()
-    return start.elapsed_time(end) * 1e3 / (reps * len(xs)), kernel
+    return start.elapsed_time(end) * 1e3 / (reps * len(xs)), kernel, fused
 
 
 def run_decode(args, hrm, dev):
@@ -369,8 +380,11 @@ def run_decode(args, hrm, dev):
         f"({us_copy:.2f} with the input copy), {touched:.1f} experts touched, {nbytes / 1e6:.1f} MB, {gbs:.0f} GB/s")
     # dominant kernel: the fused gather + gate_up + SwiGLU, timed alone from a graph of back-to-back
     # launches over the weight copies (HIP events on the stream the graph is replayed on)
-    gu_us, gu_kernel = decode_gate_up_us(layers, xs, dispatches, max(args.steps, 20))
-    gu_bytes = statistics.fmean(n * 2 * i * h * 2 for n in distinct) + t * k * (h + i) * 2
+    gu_us, gu_kernel, gu_fused = decode_gate_up_us(layers, xs, dispatches, max(args.steps, 20))
+    # touched experts' gate/up weights, the gathered rows and the act rows; the one-launch kernel also
+    # reads the logits
+    gu_bytes = (statistics.fmean(n * 2 * i * h * 2 for n in distinct) + t * k * (h + i) * 2
+                + (t * e * 2 if gu_fused else 0))
     gu_gbs = gu_bytes / (gu_us * 1e-6) / 1e9
     log(f"decode T={t}: gate_up kernel {gu_kernel} {gu_us:.2f} us, {gu_bytes / 1e6:.1f} MB, {gu_gbs:.0f} GB/s")
     result = {
@@ -395,7 +409,8 @@ def run_decode(args, hrm, dev):
         "us_with_input_copy": round(us_copy, 3),
         "layer_hbm": {"bytes_per_step": int(nbytes), "achieved_gbs": round(gbs, 1),
                       "frac": round(gbs / PEAK_HBM_GBS, 4), "experts_touched": touched},
-        "roofline": {"kernel": f"{gu_kernel} (fused gather + gate_up GEMM + SwiGLU)", "bound": "hbm",
+        "roofline": {"kernel": f"{gu_kernel} ({'router, dispatch, ' if gu_fused else ''}fused gather + gate_up GEMM "
+                               f"+ SwiGLU)", "bound": "hbm",
                      "achieved": round(gu_gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
                      "frac": round(gu_gbs / PEAK_HBM_GBS, 4), "traffic": None,
                      "bytes_per_launch": int(gu_bytes), "avg_launch_us": round(gu_us, 3)},

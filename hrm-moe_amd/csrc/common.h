@@ -89,6 +89,11 @@ const Config& config();
 // value is malformed (that knob then keeps its default).
 int reload_config();
 
+// Records the kernel instantiation the latest launch of a GEMM kind used
+// (0 NT, 1 gate/up, 2 NN), read back by hrm_moe_last_gemm_kernel; kernels
+// outside grouped_gemm.hip that do a kind's work record themselves here.
+void set_last_gemm_kernel(int kind, const char* name);
+
 // Second dispatch stage (permute.hip), after a rank step that wrote rank[R] and
 // counts[nb][E+1] for rank blocks of SB slots: one scan + scatter launch.
 int dispatch_from_ranks(const int64_t* topk_idx, int64_t R, int E, int k, int SB, int nb, const int32_t* rank,

@@ -20,6 +20,8 @@
 // invalidate) took 34-52 us per layer at T = 1 against 19.8 us for the three
 // launches, because each hand-over between workgroups on different XCDs
 // costs several dependent memory round trips.
+#include <stdio.h>
+
 #include "common.h"
 #include "route_wave.h"
 
@@ -231,6 +233,10 @@ extern "C" int hrm_moe_router_gate_up_decode(const void* logits, int logits_dtyp
   // K chunks per wave (4 waves split H in 32-wide chunks), all in flight at once
   const int need = (int)((hidden_size / 32 + 3) / 4);
   const int cpw = need <= 4 ? 4 : (need <= 8 ? 8 : (need <= 12 ? 12 : 16));
+  char name[96];
+  snprintf(name, sizeof(name), "router_gate_up_decode_kernel<%s, %d, %d>",
+           dtype == HRM_MOE_BF16 ? "hrm::BF16" : "hrm::F16", (int)top_k, cpw);
+  hrm::set_last_gemm_kernel(1, name);
 #define HRM_RG(TR_)                                                                            \
   do {                                                                                         \
     if (top_k == 2) return hrm::launch_router_gate_up_decode<TR_, 2>(a, cpw, grid, stream);    \

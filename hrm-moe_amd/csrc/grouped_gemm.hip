@@ -2413,6 +2413,13 @@ int launch_gate_wgrad(const void* dlogits, const void* hidden, int64_t T, int E,
 }  // namespace
 }  // namespace hrm
 
+namespace hrm {
+void set_last_gemm_kernel(int kind, const char* name) {
+  if (kind < 0 || kind > 2 || !name) return;
+  snprintf(g_last_kernel[kind], sizeof(g_last_kernel[kind]), "%s", name);
+}
+}  // namespace hrm
+
 extern "C" const char* hrm_moe_last_gemm_kernel(int kind) {
   if (kind < 0 || kind > 2) return "";
   return hrm::g_last_kernel[kind];

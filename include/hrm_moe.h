@@ -70,8 +70,9 @@ int hrm_moe_cu_margin(void);
 /*
  * Diagnostic, with no counterpart in the reference: the kernel instantiation
  * the latest M-grouped GEMM launch of `kind` used (0 = NT, the down
- * projection and forward grouped linear; 1 = gather + gate_up + SwiGLU;
- * 2 = NN, dgrad), as it appears inside a profiler's demangled kernel name,
+ * projection and forward grouped linear; 1 = gather + gate_up + SwiGLU,
+ * including hrm_moe_router_gate_up_decode; 2 = NN, dgrad), as it appears
+ * inside a profiler's demangled kernel name,
  * e.g. "mgemm_dma_kernel<hrm::BF16, 1, 128, 128, 2, 4, 64, 0, false>".
  * Empty before the first launch of that kind.  Lets a benchmark check that a
  * counter summary describes the kernel it timed.
