@@ -18,8 +18,9 @@
 // measured slower: workgroups that wait for every gate/up result (a counter in
 // memory, the act rows read through coherent loads or after an L2
 // invalidate) took 34-52 us per layer at T = 1 against 19.8 us for the three
-// launches, because each hand-over between workgroups on different XCDs
-// costs several dependent memory round trips.
+// launches (everything after the gate GEMM, graphs of 8 layers), because each
+// hand-over between workgroups on different XCDs costs several dependent
+// memory round trips.
 #include <stdio.h>
 
 #include "common.h"
@@ -44,7 +45,7 @@ struct DecodeArgs {
   int64_t* sort_idx;          // [T k] or null
   int32_t* slot_to_row;       // [T k]
   uint16_t* act;              // [T k, I], rows in dispatch order
-  int ldt, T, E, k, norm, H, I;
+  int ldt, T, E, norm, H, I;  // top-k is the kernel's SLOTS
 };
 
 template <typename TR, int SLOTS, int CPW>
@@ -223,7 +224,6 @@ extern "C" int hrm_moe_router_gate_up_decode(const void* logits, int logits_dtyp
   a.ldt = logits_dtype;
   a.T = (int)num_tokens;
   a.E = num_experts;
-  a.k = top_k;
   a.norm = norm_topk_prob ? 1 : 0;
   a.H = (int)hidden_size;
   a.I = (int)inter_size;
