@@ -8,9 +8,9 @@
 // decode-size router, so the routing is the same bits) and builds the
 // dispatch in LDS; workgroup 0 also writes the router and dispatch outputs.
 // Workgroup (j, cb) then runs the decode-size grouped GEMM's weight-streaming
-// step (mgemm_skinny_kernel with one 16-row block and every K chunk in
-// flight) for the j-th expert with rows and output columns [16 cb, 16 cb + 16),
-// with the SwiGLU epilogue.  The down projection and the combine follow in
+// step (skinny_step.h, as mgemm_skinny_kernel runs it with one 16-row block
+// and every K chunk in flight) for the j-th expert with rows and output
+// columns [16 cb, 16 cb + 16), with the SwiGLU epilogue.  The down projection and the combine follow in
 // one more launch (hrm_moe_down_combine_decode), which reads act after this
 // kernel has ended.
 //
@@ -25,6 +25,7 @@
 
 #include "common.h"
 #include "route_wave.h"
+#include "skinny_step.h"
 
 namespace hrm {
 namespace {
@@ -57,7 +58,7 @@ __global__ __launch_bounds__(256) void router_gate_up_decode_kernel(DecodeArgs a
   __shared__ int32_t s_tok[kDecMaxSlots];  // row -> token
   __shared__ int32_t s_cnt[65];            // bucket -> rows
   __shared__ int32_t s_off[65];            // bucket -> first row
-  __shared__ floatx4 red[4 * 2 * 64];
+  __shared__ SkinnyRed<true, 1> red;
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -129,43 +130,12 @@ __global__ __launch_bounds__(256) void router_gate_up_decode_kernel(DecodeArgs a
     const int kc0 = wave * nc / 4, kc1 = (wave + 1) * nc / 4;
     int r = rs + (lane & 15);
     r = r < re ? r : re - 1;  // rows past the expert repeat a valid one; their columns are never stored
-    const uint16_t* xr = a.x + (int64_t)s_tok[r] * K + (lane >> 4) * 8;
-    floatx4 ag = floatx4{0.f, 0.f, 0.f, 0.f}, au = floatx4{0.f, 0.f, 0.f, 0.f};
-    if (kc1 > kc0) {
-      u32x4 bg[CPW], bu[CPW], bx[CPW];
-#pragma unroll
-      for (int u = 0; u < CPW; ++u) {
-        const int kk = (kc0 + u < kc1 ? kc0 + u : kc1 - 1) * 32;
-        bg[u] = ld16(wg + kk);
-        bu[u] = ld16(wu + kk);
-        bx[u] = ld16(xr + kk);
-      }
-#pragma unroll
-      for (int u = 0; u < CPW; ++u) {
-        if (kc0 + u < kc1) {
-          ag = TR::mfma16(bg[u], bx[u], ag);
-          au = TR::mfma16(bu[u], bx[u], au);
-        }
-      }
-    }
-    red[(wave * 2 + 0) * 64 + lane] = ag;
-    red[(wave * 2 + 1) * 64 + lane] = au;
+    const uint16_t* const xr[1] = {a.x + (int64_t)s_tok[r] * K + (lane >> 4) * 8};
+    floatx4 ag[1] = {floatx4{0.f, 0.f, 0.f, 0.f}}, au[1] = {floatx4{0.f, 0.f, 0.f, 0.f}};
+    skinny_chunks<TR, true, 1, CPW>(wg, wu, xr, kc0, kc1, ag, au);
+    skinny_publish<true, 1>(red, wave, lane, ag, au);
     __syncthreads();
-    if (wave == 0) {  // the 4 K quarters in wave order; lane l holds columns c0 + 4 (l/16) + v of row l % 16
-      floatx4 gs = red[lane], us = red[64 + lane];
-#pragma unroll
-      for (int w = 1; w < 4; ++w) {
-        gs += red[(w * 2 + 0) * 64 + lane];
-        us += red[(w * 2 + 1) * 64 + lane];
-      }
-      const int row = rs + (lane & 15);
-      if (row < re) {
-        float o[4];
-#pragma unroll
-        for (int v = 0; v < 4; ++v) o[v] = swiglu_fast<TR>(gs[v], us[v]);
-        st8(a.act + (int64_t)row * N + c0 + (lane >> 4) * 4, pack4<TR>(o[0], o[1], o[2], o[3]));
-      }
-    }
+    skinny_store<TR, true, 1>(red, wave, lane, rs, re, a.act, N, c0);
   }
 }
 

@@ -28,6 +28,7 @@
 #include <stdlib.h>
 
 #include "common.h"
+#include "skinny_step.h"
 
 namespace hrm {
 namespace {
@@ -1441,7 +1442,9 @@ __global__ __launch_bounds__(NW * 64, NW == 4 ? 2 : 1) void mgemm_dma_kernel(con
   wait_vmcnt<0>();
 }
 
-// Skinny M-grouped GEMM for decode-sized inputs (a few rows per expert).
+// Skinny M-grouped GEMM for decode-sized inputs (a few rows per expert).  Its
+// load + MFMA step with every K chunk in flight and its epilogue are
+// skinny_step.h's, shared with the decode kernel that also routes.
 // Workgroup (e, cb) computes output columns [16 cb, 16 cb + 16) for every row
 // of expert e with v_mfma_f32_16x16x32: the 16 weight rows are the MFMA A
 // operand and up to 16 rows of the expert the B operand, both loaded from
@@ -1468,7 +1471,7 @@ __global__ __launch_bounds__(256) void mgemm_skinny_kernel(const uint16_t* __res
                                                            int cblk_n) {
   static_assert(KIND == KIND_NT || KIND == KIND_GATHER_SWIGLU, "skinny kernel: NT or gate/up");
   constexpr bool SW = KIND == KIND_GATHER_SWIGLU;
-  __shared__ floatx4 red[4][NRB][SW ? 2 : 1][64];
+  __shared__ SkinnyRed<SW, NRB> red;
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int j = blockIdx.x / cblk_n;  // rank of this group's expert among the experts with rows
@@ -1526,27 +1529,7 @@ __global__ __launch_bounds__(256) void mgemm_skinny_kernel(const uint16_t* __res
       au[rb] = floatx4{0.f, 0.f, 0.f, 0.f};
     }
     if constexpr (CPW > 0) {
-      if (kc1 > kc0) {
-        u32x4 bg[CPW], bu[CPW], bx[CPW][NRB];
-#pragma unroll
-        for (int u = 0; u < CPW; ++u) {
-          const int k = (kc0 + u < kc1 ? kc0 + u : kc1 - 1) * 32;
-          bg[u] = ld16(wg + k);
-          if constexpr (SW) bu[u] = ld16(wu + k);
-#pragma unroll
-          for (int rb = 0; rb < NRB; ++rb) bx[u][rb] = ld16(xr[rb] + k);
-        }
-#pragma unroll
-        for (int u = 0; u < CPW; ++u) {
-          if (kc0 + u < kc1) {
-#pragma unroll
-            for (int rb = 0; rb < NRB; ++rb) {
-              ag[rb] = TR::mfma16(bg[u], bx[u][rb], ag[rb]);
-              if constexpr (SW) au[rb] = TR::mfma16(bu[u], bx[u][rb], au[rb]);
-            }
-          }
-        }
-      }
+      skinny_chunks<TR, SW, NRB, CPW>(wg, wu, xr, kc0, kc1, ag, au);
     } else if (kc1 > kc0) {
       u32x4 bg[PD], bu[PD], bx[PD][NRB];
       // loads of chunk kc into ring slot u; chunks past the wave's range reload its last one
@@ -1573,30 +1556,10 @@ __global__ __launch_bounds__(256) void mgemm_skinny_kernel(const uint16_t* __res
         }
       }
     }
-#pragma unroll
-    for (int rb = 0; rb < NRB; ++rb) {
-      red[wave][rb][0][lane] = ag[rb];
-      if constexpr (SW) red[wave][rb][1][lane] = au[rb];
-    }
+    skinny_publish<SW, NRB>(red, wave, lane, ag, au);
     __syncthreads();
-    // waves 0..NRB-1 reduce one column block each: the 4 K quarters in wave order
-    if (wave < NRB) {
-      const int rb = wave;
-      floatx4 g = red[0][rb][0][lane], u = floatx4{0.f, 0.f, 0.f, 0.f};
-      if constexpr (SW) u = red[0][rb][1][lane];
-#pragma unroll
-      for (int w = 1; w < 4; ++w) {
-        g += red[w][rb][0][lane];
-        if constexpr (SW) u += red[w][rb][1][lane];
-      }
-      const int r = p + rb * 16 + (lane & 15);  // D: lane l holds rows c0 + 4 (l/16) + v of column l % 16
-      if (r < re) {
-        float o[4];
-#pragma unroll
-        for (int v = 0; v < 4; ++v) o[v] = SW ? swiglu_fast<TR>(g[v], u[v]) : g[v];
-        st8(C + (int64_t)r * N + c0 + (lane >> 4) * 4, pack4<TR>(o[0], o[1], o[2], o[3]));
-      }
-    }
+    // waves 0..NRB-1 reduce one row block each: the 4 K quarters in wave order
+    skinny_store<TR, SW, NRB>(red, wave, lane, p, re, C, N, c0);
     __syncthreads();  // red[] is reused by the next pass
   }
 }
