@@ -37,7 +37,8 @@ __device__ __forceinline__ void store_weight(void* p, int dt, int64_t i, float w
 }
 
 // Routes token t (row t of logits [*, E]) with the calling wave; `active`
-// false for a wave without a token (it still passes both barriers).  Every
+// false for a wave without a token (it still passes both barriers, then
+// returns my_i = 0, my_w = 0).  Every
 // wave of the workgroup must call this together: it holds two workgroup
 // barriers.  s_ck[64], s_sk[SLOTS], s_si[SLOTS]: this wave's LDS scratch.
 // probs (may be null): the wave writes the token's E probabilities.
@@ -77,6 +78,13 @@ __device__ __forceinline__ void route_token_wave(const void* __restrict__ logits
     s_si[rank] = key != 0u ? lane : 0x7fffffff;
   }
   __syncthreads();
+  my_i = 0;
+  my_w = 0.0f;
+  // A wave without a token is done: its keys are all equal (zero), so it would
+  // take the tie branch and run the whole ordering network, and its
+  // workgroup's next barrier would wait for that (the one-launch decode kernel
+  // at one token: 3.3 of its 12 us).
+  if (!active) return;
   uint32_t sk[SLOTS];
   int si[SLOTS];
 #pragma unroll
@@ -107,8 +115,6 @@ __device__ __forceinline__ void route_token_wave(const void* __restrict__ logits
 #pragma unroll
     for (int j = 0; j < SLOTS; ++j) w[j] = w[j] / sum;
   }
-  my_i = 0;
-  my_w = 0.0f;
 #pragma unroll
   for (int j = 0; j < SLOTS; ++j) {
     my_i = lane == j ? gi[j] : my_i;
