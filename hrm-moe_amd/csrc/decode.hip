@@ -4,9 +4,11 @@
 // (softmax router + top-k), :312-322 (dispatch) and :325-329 (gate/up grouped
 // linear + SwiGLU).  At these sizes each of them is a few microseconds of
 // latency, so the router launch costs as much as its work.  Here every
-// workgroup routes the tokens itself (route_token_wave, the code of the
-// decode-size router, so the routing is the same bits) and builds the
-// dispatch in LDS; workgroup 0 also writes the router and dispatch outputs.
+// workgroup selects the tokens' experts itself (route_token_select, the code
+// of the decode-size router, so the routing is the same bits), derives the
+// dispatch rows from the selection masks and issues its weight loads at once;
+// workgroup 0 also finishes the routing (route_token_finish: torch's order and
+// the weights) and writes the router and dispatch outputs while its loads fly.
 // Workgroup (j, cb) then runs the decode-size grouped GEMM's weight-streaming
 // step (skinny_step.h, as mgemm_skinny_kernel runs it with one 16-row block
 // and every K chunk in flight) for the j-th expert with rows and output
@@ -31,7 +33,6 @@ namespace hrm {
 namespace {
 
 constexpr int kDecMaxTokens = 2;
-constexpr int kDecMaxSlots = kDecMaxTokens * 8;
 
 struct DecodeArgs {
   const void* logits;         // [T, E] in ldt
@@ -54,10 +55,7 @@ __global__ __launch_bounds__(256) void router_gate_up_decode_kernel(DecodeArgs a
   __shared__ uint64_t s_ck[4][64];
   __shared__ uint32_t s_sk[4][SLOTS];
   __shared__ int32_t s_si[4][SLOTS];
-  __shared__ int32_t s_e[kDecMaxSlots];    // slot -> bucket: its expert, or E for an id outside [0, E)
-  __shared__ int32_t s_tok[kDecMaxSlots];  // row -> token
-  __shared__ int32_t s_cnt[65];            // bucket -> rows
-  __shared__ int32_t s_off[65];            // bucket -> first row
+  __shared__ uint64_t s_sel[4];  // token -> its selected experts, as a bit mask
   __shared__ SkinnyRed<true, 1> red;
 
   const int tid = threadIdx.x;
@@ -67,76 +65,76 @@ __global__ __launch_bounds__(256) void router_gate_up_decode_kernel(DecodeArgs a
   const int T = a.T, E = a.E;
   const bool writer = blockIdx.x == 0;
 
-  // ---- routing: wave w routes token w (waves past T pass the barriers idle)
-  int my_i;
-  float my_w;
-  route_token_wave<SLOTS, true>(a.logits, a.ldt, wave, wave < T, E, k, a.norm, writer ? a.probs : nullptr,
-                                s_ck[wave], s_sk[wave], s_si[wave], my_i, my_w);
-  if (wave < T && lane < k) {
-    const int ls = wave * k + lane;
-    s_e[ls] = (my_i >= 0 && my_i < E) ? my_i : E;
-    if (writer) {
-      a.idx_out[ls] = (int64_t)my_i;
-      a.w_out[ls] = TR::from_f(my_w);
-    }
-  }
-  __syncthreads();
+  // ---- selection: wave w selects token w's experts (waves past T pass the barriers idle)
+  route_token_select<SLOTS, true>(a.logits, a.ldt, wave, wave < T, E, k, writer ? a.probs : nullptr, s_ck[wave],
+                                  s_sk[wave], s_si[wave], &s_sel[wave]);
+  // Rows in dispatch order are expert-major and, within an expert, in flat slot
+  // order (token 0's row before token 1's), so the masks give every row: expert
+  // e's rows start at the number of selected slots with a smaller expert.  (Each
+  // token selects k distinct experts with nonzero keys, all inside [0, E): E >= k
+  // experts have a nonzero key and rank above the padding lanes.)
+  const uint64_t sel0 = s_sel[0];
+  const uint64_t sel1 = T > 1 ? s_sel[1] : 0ull;
+  auto rows_below = [&](int e) __attribute__((always_inline)) -> int {
+    const uint64_t below = e >= 64 ? ~0ull : ((1ull << e) - 1ull);
+    return __popcll(sel0 & below) + __popcll(sel1 & below);
+  };
 
-  // ---- dispatch: stable order of the R = T k slots by bucket (as the router's counting sort)
-  const int R = T * k;
-  if (tid < R) {
-    const int b = s_e[tid];
-    int dst = 0;
-    for (int s2 = 0; s2 < R; ++s2) {
-      const int b2 = s_e[s2];
-      dst += (b2 < b || (b2 == b && s2 < tid)) ? 1 : 0;
-    }
-    s_tok[dst] = tid / k;
-    if (writer) {
-      a.sorted_token_idx[dst] = tid / k;
-      if (a.sort_idx) a.sort_idx[dst] = tid;
-      a.slot_to_row[tid] = dst;
-    }
-  }
-  if (tid <= E) {
-    int cnt = 0, before = 0;
-    for (int s2 = 0; s2 < R; ++s2) {
-      cnt += s_e[s2] == tid ? 1 : 0;
-      before += s_e[s2] < tid ? 1 : 0;
-    }
-    s_cnt[tid] = cnt;
-    s_off[tid] = before;
-    if (writer) {
-      if (tid < E) a.tokens_per_expert[tid] = cnt;
-      a.expert_offsets[tid] = before;
-    }
-  }
-  __syncthreads();
-
-  // ---- gate/up: expert j (the j-th with rows, ascending id), columns [c0, c0 + 16)
+  // ---- gate/up: expert j (the j-th with rows, ascending id), columns [c0, c0 + 16).
+  // Its loads go out first; workgroup 0's routing outputs are computed while they fly.
+  const uint64_t any = sel0 | sel1;
   const int cblk = a.I / 16;
   const int j = blockIdx.x / cblk;
   const int c0 = (blockIdx.x - j * cblk) * 16;
-  const uint64_t nz = __ballot(lane < E && s_cnt[lane] > 0);
-  if (j < __popcll(nz)) {  // uniform over the workgroup
-    const int my_rank = __popcll(nz & ((1ull << lane) - 1ull));
-    const uint64_t hit = __ballot(((nz >> lane) & 1ull) && my_rank == j);
+  const bool has = j < __popcll(any);  // uniform over the workgroup
+  const int N = a.I, K = a.H;
+  const int nc = K / 32;
+  const int kc0 = wave * nc / 4, kc1 = (wave + 1) * nc / 4;
+  int rs = 0, re = 0;
+  SkinnyChunks<TR, true, 1, CPW> ch;
+  if (has) {
+    const int my_rank = __popcll(any & ((1ull << lane) - 1ull));
+    const uint64_t hit = __ballot(((any >> lane) & 1ull) && my_rank == j);
     const int e = __ffsll((unsigned long long)hit) - 1;
-    const int rs = s_off[e], re = rs + s_cnt[e];
-    const int N = a.I, K = a.H;
+    const int b0 = (int)((sel0 >> e) & 1ull), b1 = (int)((sel1 >> e) & 1ull);
+    rs = rows_below(e);
+    re = rs + b0 + b1;
+    int rr = lane & 15;
+    rr = rr < re - rs ? rr : re - rs - 1;  // rows past the expert repeat a valid one; their columns are never stored
+    const int tok = (b0 && b1) ? rr : (b0 ? 0 : 1);
     const uint16_t* wg = a.w_gu + ((int64_t)e * 2 * N + c0 + (lane & 15)) * K + (lane >> 4) * 8;
     const uint16_t* wu = wg + (int64_t)N * K;
-    const int nc = K / 32;
-    const int kc0 = wave * nc / 4, kc1 = (wave + 1) * nc / 4;
-    int r = rs + (lane & 15);
-    r = r < re ? r : re - 1;  // rows past the expert repeat a valid one; their columns are never stored
-    const uint16_t* const xr[1] = {a.x + (int64_t)s_tok[r] * K + (lane >> 4) * 8};
-    floatx4 ag[1] = {floatx4{0.f, 0.f, 0.f, 0.f}}, au[1] = {floatx4{0.f, 0.f, 0.f, 0.f}};
-    skinny_chunks<TR, true, 1, CPW>(wg, wu, xr, kc0, kc1, ag, au);
-    skinny_publish<true, 1>(red, wave, lane, ag, au);
-    __syncthreads();
-    skinny_store<TR, true, 1>(red, wave, lane, rs, re, a.act, N, c0);
+    const uint16_t* const xr[1] = {a.x + (int64_t)tok * K + (lane >> 4) * 8};
+    ch.load(wg, wu, xr, kc0, kc1);
   }
+
+  if (writer) {
+    // torch's output order and the weights of each token's k slots, then the dispatch tensors
+    int my_i;
+    float my_w;
+    route_token_finish<SLOTS, true>(wave < T, k, a.norm, s_sk[wave], s_si[wave], my_i, my_w);
+    if (wave < T && lane < k) {
+      const int ls = wave * k + lane;
+      a.idx_out[ls] = (int64_t)my_i;
+      a.w_out[ls] = TR::from_f(my_w);
+      const int dst = rows_below(my_i) + ((wave == 1 && ((sel0 >> my_i) & 1ull)) ? 1 : 0);
+      a.sorted_token_idx[dst] = wave;
+      if (a.sort_idx) a.sort_idx[dst] = ls;
+      a.slot_to_row[ls] = dst;
+    }
+    if (tid <= E) {
+      if (tid < E) a.tokens_per_expert[tid] = (int64_t)(((sel0 >> tid) & 1ull) + ((sel1 >> tid) & 1ull));
+      a.expert_offsets[tid] = rows_below(tid);
+    }
+  }
+
+  if (has) {
+    floatx4 ag[1] = {floatx4{0.f, 0.f, 0.f, 0.f}}, au[1] = {floatx4{0.f, 0.f, 0.f, 0.f}};
+    ch.mma(kc0, kc1, ag, au);
+    skinny_publish<true, 1>(red, wave, lane, ag, au);
+  }
+  __syncthreads();
+  if (has) skinny_store<TR, true, 1>(red, wave, lane, rs, re, a.act, N, c0);
 }
 
 template <typename TR, int SLOTS>

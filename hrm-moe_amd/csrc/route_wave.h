@@ -36,21 +36,20 @@ __device__ __forceinline__ void store_weight(void* p, int dt, int64_t i, float w
   else reinterpret_cast<float*>(p)[i] = w;
 }
 
-// Routes token t (row t of logits [*, E]) with the calling wave; `active`
-// false for a wave without a token (it still passes both barriers, then
-// returns my_i = 0, my_w = 0).  Every
-// wave of the workgroup must call this together: it holds two workgroup
-// barriers.  s_ck[64], s_sk[SLOTS], s_si[SLOTS]: this wave's LDS scratch.
+// First half of routing token t (row t of logits [*, E]) with the calling
+// wave: softmax and selection.  `active` false for a wave without a token (it
+// still passes both barriers).  Every wave of the workgroup must call this
+// together: it holds two workgroup barriers.  s_ck[64], s_sk[SLOTS],
+// s_si[SLOTS]: this wave's LDS scratch, left holding the k selected (key,
+// expert) pairs in (key desc, index asc) order for route_token_finish.
 // probs (may be null): the wave writes the token's E probabilities.
-// Result, in lanes j < k of an active wave: slot j's expert (my_i) and weight
-// (my_w, fp32 before the cast to the weight dtype).
+// s_sel (may be null): receives the set of selected experts as a bit mask,
+// visible to the whole workgroup when this returns.
 template <int SLOTS, bool KFIX>
-__device__ __forceinline__ void route_token_wave(const void* __restrict__ logits, int ldt, int64_t t, bool active,
-                                                 int E, int k_rt, int norm, float* __restrict__ probs,
-                                                 uint64_t* s_ck, uint32_t* s_sk, int32_t* s_si, int& my_i,
-                                                 float& my_w) {
+__device__ __forceinline__ void route_token_select(const void* __restrict__ logits, int ldt, int64_t t, bool active,
+                                                   int E, int k_rt, float* __restrict__ probs, uint64_t* s_ck,
+                                                   uint32_t* s_sk, int32_t* s_si, uint64_t* s_sel) {
   static_assert(SLOTS <= 8, "k <= 8");
-  constexpr int KC = KFIX ? SLOTS : 0;
   const int k = KFIX ? SLOTS : k_rt;
   const int lane = threadIdx.x & 63;
   const bool ok = active && lane < E;
@@ -77,13 +76,25 @@ __device__ __forceinline__ void route_token_wave(const void* __restrict__ logits
     s_sk[rank] = key;
     s_si[rank] = key != 0u ? lane : 0x7fffffff;
   }
+  const uint64_t sel = __ballot(rank < k && key != 0u);
+  if (s_sel != nullptr && lane == 0) *s_sel = sel;
   __syncthreads();
+}
+
+// Second half, no barriers: torch's output order and the weights of the
+// selected pairs.  Result, in lanes j < k of an active wave: slot j's expert
+// (my_i) and weight (my_w, fp32 before the cast to the weight dtype).  A wave
+// without a token returns my_i = 0, my_w = 0 at once: its keys are all equal
+// (zero), so it would take the tie branch and run the whole ordering network
+// (the one-launch decode kernel at one token waited 3.3 of its 12 us for that).
+template <int SLOTS, bool KFIX>
+__device__ __forceinline__ void route_token_finish(bool active, int k_rt, int norm, const uint32_t* s_sk,
+                                                   const int32_t* s_si, int& my_i, float& my_w) {
+  constexpr int KC = KFIX ? SLOTS : 0;
+  const int k = KFIX ? SLOTS : k_rt;
+  const int lane = threadIdx.x & 63;
   my_i = 0;
   my_w = 0.0f;
-  // A wave without a token is done: its keys are all equal (zero), so it would
-  // take the tie branch and run the whole ordering network, and its
-  // workgroup's next barrier would wait for that (the one-launch decode kernel
-  // at one token: 3.3 of its 12 us).
   if (!active) return;
   uint32_t sk[SLOTS];
   int si[SLOTS];
@@ -120,6 +131,17 @@ __device__ __forceinline__ void route_token_wave(const void* __restrict__ logits
     my_i = lane == j ? gi[j] : my_i;
     my_w = lane == j ? w[j] : my_w;
   }
+}
+
+// Both halves: routes token t with the calling wave (all waves of the
+// workgroup call it together; it holds two workgroup barriers).
+template <int SLOTS, bool KFIX>
+__device__ __forceinline__ void route_token_wave(const void* __restrict__ logits, int ldt, int64_t t, bool active,
+                                                 int E, int k_rt, int norm, float* __restrict__ probs,
+                                                 uint64_t* s_ck, uint32_t* s_sk, int32_t* s_si, int& my_i,
+                                                 float& my_w) {
+  route_token_select<SLOTS, KFIX>(logits, ldt, t, active, E, k_rt, probs, s_ck, s_sk, s_si, nullptr);
+  route_token_finish<SLOTS, KFIX>(active, k_rt, norm, s_sk, s_si, my_i, my_w);
 }
 
 }  // namespace hrm

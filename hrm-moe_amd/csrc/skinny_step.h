@@ -15,32 +15,48 @@ namespace hrm {
 
 // All of a wave's 32-wide K chunks [kc0, kc1) (at most CPW) of the weight rows
 // (wg, and wu for the up half of a gate/up pair) and of the NRB 16-row blocks
-// (xr) are loaded at once, then the MFMAs run in K order, each waiting only for
-// its own chunk.  Slots past kc1 reload the wave's last chunk and skip their
-// MFMA, so every load is in bounds and issued unconditionally.
+// (xr) are loaded at once (load), then the MFMAs run in K order, each waiting
+// only for its own chunk (mma).  Slots past kc1 reload the wave's last chunk
+// and skip their MFMA, so every load is in bounds and issued unconditionally.
+// A caller may do other work between the two while the loads are in flight.
 template <typename TR, bool SW, int NRB, int CPW>
-__device__ __forceinline__ void skinny_chunks(const uint16_t* wg, const uint16_t* wu, const uint16_t* const (&xr)[NRB],
-                                              int kc0, int kc1, floatx4 (&ag)[NRB], floatx4 (&au)[NRB]) {
-  if (kc1 <= kc0) return;
+struct SkinnyChunks {
   u32x4 bg[CPW], bu[CPW], bx[CPW][NRB];
+
+  __device__ __forceinline__ void load(const uint16_t* wg, const uint16_t* wu, const uint16_t* const (&xr)[NRB],
+                                       int kc0, int kc1) {
+    if (kc1 <= kc0) return;
 #pragma unroll
-  for (int u = 0; u < CPW; ++u) {
-    const int k = (kc0 + u < kc1 ? kc0 + u : kc1 - 1) * 32;
-    bg[u] = ld16(wg + k);
-    if constexpr (SW) bu[u] = ld16(wu + k);
+    for (int u = 0; u < CPW; ++u) {
+      const int k = (kc0 + u < kc1 ? kc0 + u : kc1 - 1) * 32;
+      bg[u] = ld16(wg + k);
+      if constexpr (SW) bu[u] = ld16(wu + k);
 #pragma unroll
-    for (int rb = 0; rb < NRB; ++rb) bx[u][rb] = ld16(xr[rb] + k);
+      for (int rb = 0; rb < NRB; ++rb) bx[u][rb] = ld16(xr[rb] + k);
+    }
   }
+
+  __device__ __forceinline__ void mma(int kc0, int kc1, floatx4 (&ag)[NRB], floatx4 (&au)[NRB]) const {
+    if (kc1 <= kc0) return;
 #pragma unroll
-  for (int u = 0; u < CPW; ++u) {
-    if (kc0 + u < kc1) {
+    for (int u = 0; u < CPW; ++u) {
+      if (kc0 + u < kc1) {
 #pragma unroll
-      for (int rb = 0; rb < NRB; ++rb) {
-        ag[rb] = TR::mfma16(bg[u], bx[u][rb], ag[rb]);
-        if constexpr (SW) au[rb] = TR::mfma16(bu[u], bx[u][rb], au[rb]);
+        for (int rb = 0; rb < NRB; ++rb) {
+          ag[rb] = TR::mfma16(bg[u], bx[u][rb], ag[rb]);
+          if constexpr (SW) au[rb] = TR::mfma16(bu[u], bx[u][rb], au[rb]);
+        }
       }
     }
   }
+};
+
+template <typename TR, bool SW, int NRB, int CPW>
+__device__ __forceinline__ void skinny_chunks(const uint16_t* wg, const uint16_t* wu, const uint16_t* const (&xr)[NRB],
+                                              int kc0, int kc1, floatx4 (&ag)[NRB], floatx4 (&au)[NRB]) {
+  SkinnyChunks<TR, SW, NRB, CPW> c;
+  c.load(wg, wu, xr, kc0, kc1);
+  c.mma(kc0, kc1, ag, au);
 }
 
 // Partial sums of the 4 waves, [wave][row block][gate, up][lane].
