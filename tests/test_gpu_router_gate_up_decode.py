@@ -59,6 +59,27 @@ def test_router_gate_up_decode_matches_two_launches(cuda, t, h, e, i, k, dtype, 
         assert torch.equal(act, cact), f"act: max |d| {(act.float() - cact.float()).abs().max().item():.3e}"
 
 
+@pytest.mark.parametrize("t,k,e", [(1, 8, 64), (2, 8, 64), (2, 4, 32), (1, 2, 8)])
+def test_router_gate_up_decode_ties(cuda, t, k, e):
+    """Logits on a coarse grid, so many probabilities are equal and the top-k set is decided by ties: the
+    kernel's selection (a bitwise search for the k-th largest key, then the lowest indices among the equal
+    ones) must give the router's rank-order set, and all outputs the router's bits."""
+    h, i = 256, 64
+    x, wg, wgu, _ = _inputs(500 + t + k, t, h, e, i, torch.bfloat16, cuda)
+    gen = torch.Generator().manual_seed(600 + t + k)
+    for levels in (2, 3, 5):
+        logits = torch.randint(0, levels, (t, e), generator=gen).to(torch.bfloat16).to(cuda) * 0.5
+        probs, w, idx, d, act = ops.router_gate_up_decode(logits, x, wgu, k, True, want_probs=True,
+                                                          want_sort_idx=True)
+        cprobs, cw, cidx, cd = ops.router_topk_dispatch(logits, k, True, x.dtype, want_probs=True, want_sort_idx=True)
+        cact = ops.gate_up_swiglu(x, cd, wgu)
+        assert torch.equal(idx, cidx), f"routing indices, {levels} logit levels"
+        assert torch.equal(w, cw) and torch.equal(probs, cprobs)
+        for name in ("tokens_per_expert", "expert_offsets", "sorted_token_idx", "slot_to_row", "sort_idx"):
+            assert torch.equal(getattr(d, name), getattr(cd, name)), name
+        assert torch.equal(act, cact)
+
+
 @pytest.mark.parametrize("t", [1, 2])
 def test_decode_module_and_graph(cuda, t):
     """The module takes the fused launch at one or two tokens: its output matches the oracle within bf16
