@@ -11,6 +11,7 @@
 //  * softmax: torch's persistent softmax over a row of up to 64 values reduces
 //    across the wave with an xor butterfly at distances 32 ... 1 (maximum,
 //    then the sum of exp(x - max)); exp is expf and the division is IEEE.
+//    The same sums are formed here with cheaper lane moves (route_token_select).
 //    Lanes past E hold -inf, so exp gives 0 and the sums are unchanged.
 //  * top-k: the rank of each lane's (p, 63 - lane) pair among the wave's 64
 //    unique pairs selects the k largest in (value desc, index asc) order.
@@ -23,6 +24,23 @@
 #include "topk_order.h"
 
 namespace hrm {
+
+// Value of the lane at distance D inside the row (D = 1, 2: xor; D = 4, 8:
+// rotation within a row of 16 lanes).
+template <int D>
+__device__ __forceinline__ uint32_t xlane(uint32_t x) {
+  constexpr int ctrl = D == 1 ? 0xB1 : D == 2 ? 0x4E : D == 4 ? 0x124 : 0x128;  // quad_perm / row_ror
+  return (uint32_t)__builtin_amdgcn_mov_dpp((int)x, ctrl, 0xF, 0xF, false);
+}
+template <int D>
+__device__ __forceinline__ float xlanef(float x) {
+  return __uint_as_float(xlane<D>(__float_as_uint(x)));
+}
+// Value of lane ^ 16 (within each half of the wave), by swizzle: and-mask 31,
+// or-mask 0, xor-mask 16.
+__device__ __forceinline__ float xor16f(float x) {
+  return __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(x), 0x401F));
+}
 
 __device__ __forceinline__ float load_logit(const void* p, int dt, int64_t i) {
   if (dt == HRM_MOE_BF16) return BF16::to_f(reinterpret_cast<const uint16_t*>(p)[i]);
@@ -54,13 +72,28 @@ __device__ __forceinline__ void route_token_select(const void* __restrict__ logi
   const int lane = threadIdx.x & 63;
   const bool ok = active && lane < E;
   const float x = ok ? load_logit(logits, ldt, t * E + lane) : -INFINITY;
+  // xor butterfly at distances 32 ... 1 (torch's order): a permute for 32, a
+  // swizzle for 16 (lane ^ 16 within each half), then DPP row moves.  Rotation
+  // by 8 within a row of 16 is xor 8; at the distance-4 step every lane's value
+  // depends only on its index mod 8, so rotation by 4 reads the same value as
+  // xor 4; the sums are the butterfly's, bit for bit (and any order gives the
+  // same maximum).  Six permutes through LDS, each waited for before the next,
+  // took about 0.4 us of the one-launch decode kernel.
   float mx = x;
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
+  mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+  mx = fmaxf(mx, xor16f(mx));
+  mx = fmaxf(mx, xlanef<8>(mx));
+  mx = fmaxf(mx, xlanef<4>(mx));
+  mx = fmaxf(mx, xlanef<2>(mx));
+  mx = fmaxf(mx, xlanef<1>(mx));
   const float s = expf(x - mx);
   float total = s;
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) total = total + __shfl_xor(total, o, 64);
+  total = total + __shfl_xor(total, 32, 64);
+  total = total + xor16f(total);
+  total = total + xlanef<8>(total);
+  total = total + xlanef<4>(total);
+  total = total + xlanef<2>(total);
+  total = total + xlanef<1>(total);
   const float p = s / total;
   if (ok && probs != nullptr) probs[t * E + lane] = p;
   const uint32_t key = ok ? (__float_as_uint(p) + 1u) : 0u;  // 0 marks "not selectable"

@@ -37,18 +37,6 @@ namespace {
 
 constexpr int kRouterMaxExperts = 128;
 
-// Value of the lane at distance D inside the row (D = 1, 2: xor; D = 4, 8:
-// rotation within a row of 16 lanes).
-template <int D>
-__device__ __forceinline__ uint32_t xlane(uint32_t x) {
-  constexpr int ctrl = D == 1 ? 0xB1 : D == 2 ? 0x4E : D == 4 ? 0x124 : 0x128;  // quad_perm / row_ror
-  return (uint32_t)__builtin_amdgcn_mov_dpp((int)x, ctrl, 0xF, 0xF, false);
-}
-template <int D>
-__device__ __forceinline__ float xlanef(float x) {
-  return __uint_as_float(xlane<D>(__float_as_uint(x)));
-}
-
 // One selection round over the row's lanes: the largest remaining key, ties
 // to the lower expert index; the winner's key is cleared in the lane that holds it.
 template <int C, int LPR>
