@@ -9,12 +9,12 @@
 // dispatch rows from the selection masks and issues its weight loads at once;
 // workgroup 0 also finishes the routing (route_token_finish: torch's order and
 // the weights) and writes the router and dispatch outputs while its loads fly.
-// Workgroup (j, cb) then runs the decode-size grouped GEMM's weight-streaming
-// step (skinny_step.h, as mgemm_skinny_kernel runs it with one 16-row block
-// and every K chunk in flight) for the j-th expert with rows and output
-// columns [16 cb, 16 cb + 16), with the SwiGLU epilogue.  The down projection and the combine follow in
-// one more launch (hrm_moe_down_combine_decode), which reads act after this
-// kernel has ended.
+// Workgroup (j, cb) runs the decode-size grouped GEMM's weight-streaming step
+// (skinny_step.h, as mgemm_skinny_kernel runs it with one 16-row block and
+// every K chunk in flight) for the j-th expert with rows and output columns
+// [16 cb, 16 cb + 16), with the SwiGLU epilogue.  The down projection and the
+// combine follow in one more launch (hrm_moe_down_combine_decode), which reads
+// act after this kernel has ended.
 //
 // Taking the down projection and the combine into this launch as well was
 // measured slower: workgroups that wait for every gate/up result (a counter in
