@@ -170,11 +170,24 @@ __global__ __launch_bounds__(256) void router_topk_kernel(const void* __restrict
   uint32_t key[C];
 #pragma unroll
   for (int j = 0; j < C; ++j) {
-    const float p = s[j] / total;
-    const int e = e0 + j;
-    const bool ok = active && e < E;
-    if (ok && probs != nullptr) probs[row * E + e] = p;
-    key[j] = ok ? (__float_as_uint(p) + 1u) : 0u;  // 0 marks "not selectable"
+    s[j] = s[j] / total;
+    const bool ok = active && e0 + j < E;
+    key[j] = ok ? (__float_as_uint(s[j]) + 1u) : 0u;  // 0 marks "not selectable"
+  }
+  // The lane's C probabilities are contiguous in the row: 16-byte stores when
+  // the lane's range lies inside the row and the rows are 16-byte aligned
+  // (16 single stores per lane took 2.6 of the router's 15 us at 16384 tokens).
+  if (probs != nullptr && active) {
+    if ((C % 4) == 0 && (E % 4) == 0 && e0 + C <= E && (reinterpret_cast<uintptr_t>(probs) & 15) == 0) {
+#pragma unroll
+      for (int v = 0; v < C / 4; ++v)
+        *reinterpret_cast<float4*>(probs + row * E + e0 + 4 * v) = float4{s[4 * v], s[4 * v + 1], s[4 * v + 2],
+                                                                          s[4 * v + 3]};
+    } else {
+#pragma unroll
+      for (int j = 0; j < C; ++j)
+        if (e0 + j < E) probs[row * E + e0 + j] = s[j];
+    }
   }
 
   // Top-k selection in (value desc, index asc) order: k rounds of a row-wide
