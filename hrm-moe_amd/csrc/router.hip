@@ -176,7 +176,7 @@ __global__ __launch_bounds__(256) void router_topk_kernel(const void* __restrict
   }
   // The lane's C probabilities are contiguous in the row: 16-byte stores when
   // the lane's range lies inside the row and the rows are 16-byte aligned
-  // (16 single stores per lane took 2.6 of the router's 15 us at 16384 tokens).
+  // (16 single stores per lane cost 2.6 us more at 16384 tokens, 64 experts).
   if (probs != nullptr && active) {
     if ((C % 4) == 0 && (E % 4) == 0 && e0 + C <= E && (reinterpret_cast<uintptr_t>(probs) & 15) == 0) {
 #pragma unroll
